@@ -1,0 +1,89 @@
+// Device helpers shared by the gfx950 kernels of this library: element conversions, MFMA atoms,
+// workgroup-id remapping. gfx950 (CDNA4) only; 64-wide wavefronts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/aklr_amd.h"
+
+namespace aklr {
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// 16-byte loads: plain (cached) and non-temporal (streamed once, kept out of the caches' way).
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ u32x4 ld16_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// fl32(1/448) = 0x3B124925 (0x1.24924ap-9): the e4m3fn quantizer multiplies amax by this constant
+// (it does not divide by 448).
+constexpr float kInv448 = 0x1.24924ap-9f;
+constexpr float kAmaxFloor = 1e-10f;
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// fp32 -> bf16 bits, round to nearest even (finite inputs; NaN stays NaN).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+// Four floats -> four e4m3fn bytes (OCP fp8 on gfx950), round to nearest even, byte 0 = a.
+// Callers clamp to +-448 first, so the conversion's overflow rule never applies.
+__device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+// Workgroup-id remap: the hardware hands consecutive workgroup ids round-robin to the 8 XCDs, so
+// id -> (id % 8) * per_xcd + id / 8 makes consecutive *logical* ids land on one XCD (one L2).
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t id, uint32_t total) {
+  constexpr uint32_t kXcd = 8;
+  if (total < kXcd || (total % kXcd) != 0) return id;
+  return (id % kXcd) * (total / kXcd) + id / kXcd;
+}
+
+// 16x16x128 F8F6F4 MFMA. FMT: 0 e4m3, 1 e5m2, 4 e2m1 (both operands). Scale bytes are e8m0;
+// 127 is 1.0. D[i][j] for i = 4*(lane/16) + r, j = lane % 16.
+template <int FMT>
+__device__ __forceinline__ f32x4 mfma16x128(const i32x8& a, const i32x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT, FMT, 0, 127, 0, 127);
+}
+
+template <int FMT, int OPSEL_A, int OPSEL_B>
+__device__ __forceinline__ f32x4 mfma16x128_scaled(const i32x8& a, const i32x8& b, const f32x4& c, int sa,
+                                                    int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT, FMT, OPSEL_A, sa, OPSEL_B, sb);
+}
+
+__device__ __forceinline__ void store_out(void* out, int64_t idx, float v, int out_dtype) {
+  if (out_dtype == AKLR_OUT_BF16)
+    reinterpret_cast<uint16_t*>(out)[idx] = (uint16_t)f32_to_bf16_bits(v);
+  else
+    reinterpret_cast<uint16_t*>(out)[idx] = (uint16_t)f32_to_f16_bits(v);
+}
+
+}  // namespace aklr
+
+#define AKLR_LAUNCH_CHECK()                          \
+  do {                                               \
+    if (hipGetLastError() != hipSuccess) return AKLR_ERR_LAUNCH; \
+  } while (0)
+
+static inline bool aklr_aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

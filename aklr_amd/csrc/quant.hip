@@ -1,0 +1,254 @@
+// Dynamic activation quantizers for gfx950: per-1x128 FP8 (fp32 scales, group-major), per-1x32
+// MXFP8 (e8m0 scales) and per-1x32 MXFP4 (e2m1 codes, e8m0 scales, row-major or aiter-shuffled).
+// All three are HBM-bound: one coalesced pass over x, amax reduced with lane shuffles inside the
+// lanes that share a group, codes and scales written once.
+#include "common.h"
+
+namespace aklr {
+
+// ---------------------------------------------------------------------------------------------
+// per_group_quant_fp8 (aklr/ops/quant/reference.py:9-28)
+// A wave covers 8 rows x one 128-wide group: 8 lanes per row, each lane 16 values as two 16-byte
+// loads (elements 8j..8j+7 and 64+8j..64+8j+7), so each load instruction reads 128 contiguous
+// bytes per row. A 256-thread workgroup covers the same 8 rows x 4 consecutive groups.
+// Scales [g, t] are group-major, so the 8 lanes j == 0 of a wave write 8 consecutive floats.
+__global__ __launch_bounds__(256) void quant_fp8_1x128_kernel(const uint16_t* __restrict__ x, int64_t xs,
+                                                              uint8_t* __restrict__ q, float* __restrict__ scales,
+                                                              int64_t rows, int64_t cols) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane >> 3, j = lane & 7;
+  const int64_t row = (int64_t)blockIdx.x * 8 + r;
+  const int64_t groups = cols >> 7;
+  const int64_t g = (int64_t)blockIdx.y * 4 + wave;
+  if (g >= groups) return;  // whole wave exits together
+  const bool active = row < rows;
+
+  u32x4 v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
+  const uint16_t* src = x + row * xs + g * 128;
+  if (active) {
+    v0 = ld16_nt(src + 8 * j);
+    v1 = ld16_nt(src + 64 + 8 * j);
+  }
+  float f[16];
+  const uint32_t w[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    f[2 * i] = bf16_lo(w[i]);
+    f[2 * i + 1] = bf16_hi(w[i]);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(f[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  amax = fmaxf(amax, __shfl_xor(amax, 4));
+  amax = fmaxf(amax, kAmaxFloor);
+  const float s = amax * kInv448;   // rounds once to fp32
+  const float inv = 1.0f / s;       // IEEE division: correctly rounded (no fast-math in this build)
+  if (!active) return;
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float a = fminf(fmaxf(f[4 * i + 0] * inv, -448.0f), 448.0f);
+    float b = fminf(fmaxf(f[4 * i + 1] * inv, -448.0f), 448.0f);
+    float c = fminf(fmaxf(f[4 * i + 2] * inv, -448.0f), 448.0f);
+    float d = fminf(fmaxf(f[4 * i + 3] * inv, -448.0f), 448.0f);
+    o[i] = pack4_e4m3(a, b, c, d);
+  }
+  uint8_t* dst = q + row * cols + g * 128;
+  *reinterpret_cast<uint2*>(dst + 8 * j) = make_uint2(o[0], o[1]);
+  *reinterpret_cast<uint2*>(dst + 64 + 8 * j) = make_uint2(o[2], o[3]);
+  if (j == 0) scales[g * rows + row] = s;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Groups of 32: 4 lanes per group, 8 values (one 16-byte load) per lane; a wave covers 16
+// consecutive groups of one row (1 KiB of bf16), a 256-thread workgroup 64 groups.
+struct Group32 {
+  float f[8];
+  float amax;  // over the 32 values of the group, shared by its 4 lanes
+};
+
+__device__ __forceinline__ Group32 load_group32(const uint16_t* src, bool active) {
+  Group32 g;
+  u32x4 v = {0, 0, 0, 0};
+  if (active) v = ld16_nt(src);
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    g.f[2 * i] = bf16_lo(w[i]);
+    g.f[2 * i + 1] = bf16_hi(w[i]);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(g.f[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  g.amax = amax;
+  return g;
+}
+
+// per_group_quant_mxfp8 (aklr/ops/quant/reference.py:31-48)
+__global__ __launch_bounds__(256) void quant_mxfp8_kernel(const uint16_t* __restrict__ x, int64_t xs,
+                                                          uint8_t* __restrict__ q, uint8_t* __restrict__ scales,
+                                                          int64_t rows, int64_t cols) {
+  const int64_t row = blockIdx.y;
+  const int64_t groups = cols >> 5;
+  const int64_t g = (int64_t)blockIdx.x * 64 + (threadIdx.x >> 2);
+  const int part = threadIdx.x & 3;
+  const bool active = g < groups;
+  Group32 v = load_group32(x + row * xs + g * 32 + part * 8, active);
+  const float amax = fmaxf(v.amax, kAmaxFloor);
+  const uint32_t raw = __float_as_uint(amax * kInv448);
+  const uint32_t e = (raw >> 23) + ((raw & 0x7FFFFFu) != 0u);  // biased exponent rounded up
+  // x / 2^(e-127) == x * 2^(127-e) exactly: 127-e is in [-120, 43] for finite bf16 inputs.
+  const float mul = __uint_as_float((254u - e) << 23);
+  if (!active) return;
+  uint32_t o[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    float a = fminf(fmaxf(v.f[4 * i + 0] * mul, -448.0f), 448.0f);
+    float b = fminf(fmaxf(v.f[4 * i + 1] * mul, -448.0f), 448.0f);
+    float c = fminf(fmaxf(v.f[4 * i + 2] * mul, -448.0f), 448.0f);
+    float d = fminf(fmaxf(v.f[4 * i + 3] * mul, -448.0f), 448.0f);
+    o[i] = pack4_e4m3(a, b, c, d);
+  }
+  *reinterpret_cast<uint2*>(q + row * cols + g * 32 + part * 8) = make_uint2(o[0], o[1]);
+  if (part == 0) scales[row * groups + g] = (uint8_t)e;
+}
+
+// e2m1 index of |v| (v already divided by the block scale, |v| <= 6): nearest grid point of
+// {0, .5, 1, 1.5, 2, 3, 4, 6}, ties to the even index -- strict '>' where the tie goes down,
+// '>=' where it goes up.
+__device__ __forceinline__ uint32_t e2m1_code(float v) {
+  const float m = fabsf(v);
+  uint32_t idx = (m > 0.25f) + (m >= 0.75f) + (m > 1.25f) + (m >= 1.75f) + (m > 2.5f) + (m >= 3.5f) + (m > 5.0f);
+  return idx | ((__float_as_uint(v) >> 28) & 8u);
+}
+
+// Byte offset of scale (row, col) in aiter's shuffled e8m0 layout over a [pr, pc] padded matrix:
+// split (pr/32, 2, 16, pc/8, 2, 4) permuted (0, 3, 5, 2, 4, 1).
+__device__ __forceinline__ int64_t shuffled_scale_offset(int64_t row, int64_t col, int64_t pc) {
+  const int64_t r0 = row >> 5, r1 = (row >> 4) & 1, r2 = row & 15;
+  const int64_t c0 = col >> 3, c2 = (col >> 2) & 1, c3 = col & 3;
+  return ((((r0 * (pc >> 3) + c0) * 4 + c3) * 16 + r2) * 2 + c2) * 2 + r1;
+}
+
+// dynamic_mxfp4_quant (aklr/ops/fused_moe/reference.py:21-37). With a shuffled scale layout the
+// grid also covers the padding rows/columns, whose scale bytes are written as 0x00.
+__global__ __launch_bounds__(256) void quant_mxfp4_kernel(const uint16_t* __restrict__ x, int64_t xs,
+                                                          uint8_t* __restrict__ q, uint8_t* __restrict__ scales,
+                                                          int64_t rows, int64_t cols, int shuffled,
+                                                          int64_t pad_cols) {
+  const int64_t row = blockIdx.y;
+  const int64_t groups = cols >> 5;
+  const int64_t g = (int64_t)blockIdx.x * 64 + (threadIdx.x >> 2);
+  const int part = threadIdx.x & 3;
+  const int64_t gcount = shuffled ? pad_cols : groups;
+  if (g >= gcount) return;  // uniform per group of 4 lanes
+  const bool active = row < rows && g < groups;
+  Group32 v = load_group32(x + (active ? row * xs + g * 32 + part * 8 : 0), active);
+  uint32_t sbyte = 0;
+  if (active) {
+    const float amax = v.amax;
+    if (__builtin_isfinite(amax)) {
+      int e;
+      const float m = frexpf(fmaxf(amax, kAmaxFloor), &e);
+      int E = e - 3 + (m > 0.75f ? 1 : 0);
+      E = E < -127 ? -127 : (E > 127 ? 127 : E);
+      // x / 2^E == x * 2^-E exactly (2^-E is representable for E in [-127, 127]; 2^-127 is the
+      // subnormal 0x00400000).
+      const float mul = E < 127 ? __uint_as_float((uint32_t)(127 - E) << 23) : __uint_as_float(0x00400000u);
+      uint32_t packed = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) packed |= e2m1_code(v.f[i] * mul) << (4 * i);
+      *reinterpret_cast<uint32_t*>(q + row * (cols >> 1) + g * 16 + part * 4) = packed;
+      sbyte = (uint32_t)(E + 127);
+    } else {
+      *reinterpret_cast<uint32_t*>(q + row * (cols >> 1) + g * 16 + part * 4) = 0u;
+      sbyte = 255u;
+    }
+  }
+  if (part == 0) {
+    if (shuffled)
+      scales[shuffled_scale_offset(row, g, pad_cols)] = (uint8_t)sbyte;
+    else
+      scales[row * groups + g] = (uint8_t)sbyte;
+  }
+}
+
+}  // namespace aklr
+
+using namespace aklr;
+
+extern "C" int aklr_abi_version(void) { return AKLR_AMD_ABI_VERSION; }
+
+extern "C" const char* aklr_status_string(int status) {
+  switch (status) {
+    case AKLR_OK: return "ok";
+    case AKLR_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case AKLR_ERR_UNSUPPORTED: return "unsupported layout or dtype";
+    case AKLR_ERR_WORKSPACE: return "workspace too small";
+    case AKLR_ERR_LAUNCH: return "kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+extern "C" int aklr_per_group_quant_fp8(const void* x, int64_t x_row_stride, void* quantized, float* scales,
+                                        int64_t n_tokens, int64_t hidden_size, hipStream_t stream) {
+  if (!x || !quantized || !scales) return AKLR_ERR_INVALID_ARGUMENT;
+  if (n_tokens < 0 || hidden_size <= 0 || hidden_size % 128 != 0 || x_row_stride < hidden_size ||
+      x_row_stride % 8 != 0)
+    return AKLR_ERR_INVALID_ARGUMENT;
+  if (!aklr_aligned16(x) || !aklr_aligned16(quantized) || (reinterpret_cast<uintptr_t>(scales) & 3u))
+    return AKLR_ERR_INVALID_ARGUMENT;
+  if (n_tokens == 0) return AKLR_OK;
+  const int64_t groups = hidden_size / 128;
+  dim3 grid((unsigned)((n_tokens + 7) / 8), (unsigned)((groups + 3) / 4));
+  if (grid.x > 0x7FFFFFFFu || grid.y > 65535u) return AKLR_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(quant_fp8_1x128_kernel, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(x),
+                     x_row_stride, static_cast<uint8_t*>(quantized), scales, n_tokens, hidden_size);
+  AKLR_LAUNCH_CHECK();
+  return AKLR_OK;
+}
+
+extern "C" int aklr_per_group_quant_mxfp8(const void* x, int64_t x_row_stride, void* quantized,
+                                          uint8_t* scales, int64_t n_tokens, int64_t hidden_size,
+                                          hipStream_t stream) {
+  if (!x || !quantized || !scales) return AKLR_ERR_INVALID_ARGUMENT;
+  if (n_tokens < 0 || hidden_size <= 0 || hidden_size % 32 != 0 || x_row_stride < hidden_size ||
+      x_row_stride % 8 != 0)
+    return AKLR_ERR_INVALID_ARGUMENT;
+  if (!aklr_aligned16(x) || !aklr_aligned16(quantized)) return AKLR_ERR_INVALID_ARGUMENT;
+  if (n_tokens == 0) return AKLR_OK;
+  if (n_tokens > 0x7FFFFFFF) return AKLR_ERR_INVALID_ARGUMENT;
+  const int64_t groups = hidden_size / 32;
+  dim3 grid((unsigned)((groups + 63) / 64), (unsigned)n_tokens);
+  hipLaunchKernelGGL(quant_mxfp8_kernel, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(x),
+                     x_row_stride, static_cast<uint8_t*>(quantized), scales, n_tokens, hidden_size);
+  AKLR_LAUNCH_CHECK();
+  return AKLR_OK;
+}
+
+extern "C" int aklr_dynamic_mxfp4_quant(const void* x, int64_t x_row_stride, uint8_t* quantized, uint8_t* scales,
+                                        int64_t n_tokens, int64_t hidden_size, int scale_layout,
+                                        hipStream_t stream) {
+  if (!x || !quantized || !scales) return AKLR_ERR_INVALID_ARGUMENT;
+  if (n_tokens < 0 || hidden_size <= 0 || hidden_size % 32 != 0 || x_row_stride < hidden_size ||
+      x_row_stride % 8 != 0)
+    return AKLR_ERR_INVALID_ARGUMENT;
+  if (scale_layout != AKLR_SCALES_ROW_MAJOR && scale_layout != AKLR_SCALES_SHUFFLED) return AKLR_ERR_UNSUPPORTED;
+  if (!aklr_aligned16(x) || (reinterpret_cast<uintptr_t>(quantized) & 3u)) return AKLR_ERR_INVALID_ARGUMENT;
+  if (n_tokens == 0) return AKLR_OK;
+  const bool shuffled = scale_layout == AKLR_SCALES_SHUFFLED;
+  const int64_t groups = hidden_size / 32;
+  const int64_t pad_rows = shuffled ? (n_tokens + 255) / 256 * 256 : n_tokens;
+  const int64_t pad_cols = shuffled ? (groups + 7) / 8 * 8 : groups;
+  if (pad_rows > 0x7FFFFFFF) return AKLR_ERR_INVALID_ARGUMENT;
+  dim3 grid((unsigned)((pad_cols + 63) / 64), (unsigned)pad_rows);
+  hipLaunchKernelGGL(quant_mxfp4_kernel, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(x),
+                     x_row_stride, quantized, scales, n_tokens, hidden_size, shuffled ? 1 : 0, pad_cols);
+  AKLR_LAUNCH_CHECK();
+  return AKLR_OK;
+}

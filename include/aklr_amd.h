@@ -1,0 +1,133 @@
+/*
+ * aklr_amd.h -- C ABI of the MI355X (gfx950) block-scaled low-precision GEMM path.
+ *
+ * Every entry point takes raw device pointers, element counts and strides, and the HIP stream
+ * to launch on. It launches kernels only: it never allocates, frees, synchronizes, or changes
+ * the current device. It returns AKLR_OK or a nonzero status (aklr_status_string names it).
+ * Entry points are stateless and may be called from any host thread with its own stream.
+ *
+ * Scratch memory (split-K partials) is brought by the caller: ask *_workspace_bytes() for the
+ * size, pass a device buffer at least that large (16-byte aligned). The library keeps nothing
+ * between calls.
+ *
+ * Each entry point replaces one kernel ABI of the reference (a TORCH_LIBRARY `run(...)` op that
+ * AKLR's HipBuilder loads); the citation is on each declaration.
+ */
+#ifndef AKLR_AMD_H
+#define AKLR_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AKLR_AMD_ABI_VERSION 1
+
+/* Status codes. */
+enum {
+    AKLR_OK = 0,
+    AKLR_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size, misaligned pointer or stride */
+    AKLR_ERR_UNSUPPORTED = 2,      /* a layout/dtype combination no kernel here serves */
+    AKLR_ERR_WORKSPACE = 3,        /* workspace smaller than *_workspace_bytes() */
+    AKLR_ERR_LAUNCH = 4            /* hipGetLastError() after the launch was not hipSuccess */
+};
+
+/* Element types. */
+enum { AKLR_FP8_E4M3FN = 0, AKLR_FP8_E5M2 = 1 };
+enum { AKLR_OUT_BF16 = 0, AKLR_OUT_F16 = 1 };
+
+/* Weight (b) layouts. PRESHUFFLE_16x16 is aiter shuffle_weight(layout=(16,16)): rows split in
+ * tiles of 16, columns in tiles of 32 bytes; tile-major, each tile stored as two 256-byte halves
+ * (bytes 0-15 then 16-31 of every row). */
+enum { AKLR_B_ROW_MAJOR = 0, AKLR_B_PRESHUFFLE_16x16 = 1 };
+
+/* e8m0 scale layouts for MXFP4. SHUFFLED is aiter shuffle_scale on scales padded with 0x00 to
+ * (256-row, 8-column) multiples. */
+enum { AKLR_SCALES_ROW_MAJOR = 0, AKLR_SCALES_SHUFFLED = 1 };
+
+int aklr_abi_version(void);
+const char* aklr_status_string(int status);
+
+/*
+ * Dynamic per-1x128 FP8 quantization.
+ * Replaces: per_group_quant_fp8 kernel ABI `run(Tensor x, Tensor(a!) quantized, Tensor(b!) scales)`
+ *   (aklr/ops/quant/impls/hip/per_group_quant_fp8_hidden_size7168/1654009925223f46.json:110),
+ *   contract aklr/ops/quant/contract.py:17-51, arithmetic aklr/ops/quant/reference.py:9-28.
+ * x: bf16 [n_tokens, hidden_size], row stride x_row_stride elements (>= hidden_size).
+ * quantized: e4m3fn [n_tokens, hidden_size] contiguous. scales: fp32 [hidden_size/128, n_tokens]
+ *   (group-major: element [g, t] at g*n_tokens + t). hidden_size % 128 == 0.
+ * Per group: amax = max(|x|) floored at 1e-10; s = amax * fl32(1/448); q = e4m3(clamp(x * (1/s), +-448)).
+ */
+int aklr_per_group_quant_fp8(const void* x, int64_t x_row_stride, void* quantized, float* scales,
+                             int64_t n_tokens, int64_t hidden_size, hipStream_t stream);
+
+/*
+ * Dynamic per-1x32 MXFP8 quantization (e4m3fn values, e8m0 scale rounded up to a power of two).
+ * Replaces: per_group_quant_mxfp8 kernel ABI `run(Tensor x, Tensor(a!) quantized, Tensor(b!) scales)`
+ *   (aklr/ops/quant/impls/hip/per_group_quant_mxfp8_hidden_size7168/8480caae0c25689c.json:110),
+ *   contract aklr/ops/quant/contract.py:54-75, arithmetic aklr/ops/quant/reference.py:31-48.
+ * scales: uint8 [n_tokens, hidden_size/32] row-major (biased exponent). hidden_size % 32 == 0.
+ */
+int aklr_per_group_quant_mxfp8(const void* x, int64_t x_row_stride, void* quantized, uint8_t* scales,
+                               int64_t n_tokens, int64_t hidden_size, hipStream_t stream);
+
+/*
+ * Dynamic MXFP4 quantization of activations (e2m1 codes two per byte, low nibble first; one e8m0
+ * scale per 32 values along the row).
+ * Replaces: aiter dynamic_mxfp4_quant as restated by aklr/ops/fused_moe/reference.py:21-37 (`_mxfp4`);
+ *   AKLR has no kernel ABI for it.
+ * quantized: uint8 [n_tokens, hidden_size/2]. scales: e8m0 bytes; scale_layout ROW_MAJOR is
+ *   [n_tokens, hidden_size/32]; SHUFFLED is the padded, shuffled aiter layout
+ *   [ceil(n_tokens/256)*256, ceil(hidden_size/32/8)*8] (the caller pre-fills nothing: padding bytes
+ *   are written as 0x00 by this call). hidden_size % 32 == 0.
+ */
+int aklr_dynamic_mxfp4_quant(const void* x, int64_t x_row_stride, uint8_t* quantized, uint8_t* scales,
+                             int64_t n_tokens, int64_t hidden_size, int scale_layout, hipStream_t stream);
+
+/*
+ * 128x128-block-scaled FP8 GEMM: out = (a * a_scale) @ (b * b_scale)^T + bias, fp32 accumulation.
+ * Replaces: gemm_a8w8_blockwise_scaled kernel ABI `run(a, b, a_scale, b_scale, scale_major_mode,
+ *   trans_b, operand_format, bias, out_dtype, out)` (aklr/ops/gemm/impls/flydsl/
+ *   gemm_a8w8_blockwise_scaled_b_shuffled_n4096_k2048/5c97ff66d898f5a1.json entry `run`),
+ *   contract aklr/ops/gemm/contract.py:211-308, arithmetic aklr/ops/gemm/reference.py:90-105.
+ * a: fp8 [m, k], row stride lda elements. b: fp8, trans_b layout [n, k]: ROW_MAJOR with row stride
+ *   ldb, or PRESHUFFLE_16x16 (contiguous, ldb ignored). a and b share fp8_dtype.
+ * a_scale: fp32, element (i, kb) at a_scale[i*sa_stride_m + kb*sa_stride_k]; this covers K-major
+ *   (stride_m = k/128, stride_k = 1), MN-major and aiter's column-major (stride_m = 1, stride_k = m).
+ * b_scale: fp32 [ceil(n/128), k/128], row stride ldbs. bias: fp32 [n] or NULL.
+ * out: [m, n] bf16 or f16 (out_dtype), row stride ldo.
+ * k % 128 == 0, n % 16 == 0. All pointers 16-byte aligned; lda, ldb, ldo multiples of 16 bytes.
+ */
+size_t aklr_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k);
+int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void* b, int64_t ldb, const float* a_scale,
+                              int64_t sa_stride_m, int64_t sa_stride_k, const float* b_scale, int64_t ldbs,
+                              const float* bias, void* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
+                              int fp8_dtype, int b_layout, int out_dtype, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * MXFP4 GEMM: out = (a * 2^(a_scale-127)) @ (b * 2^(b_scale-127))^T + bias (alpha 1, beta 0).
+ * Replaces: gemm_a4w4_mxfp4 kernel ABI `run(a, b, a_scale, b_scale, trans_b, operand_format, alpha,
+ *   beta, bias, out_dtype, out)` (call keys per aklr/core/contract/op.py:511-558; no kernel is
+ *   committed in the reference), contract aklr/ops/gemm/contract.py:315-390, arithmetic
+ *   aklr/ops/gemm/reference.py:108-122.
+ * a: packed e2m1 [m, k/2] bytes (low nibble first), row stride lda bytes. b: [n, k/2] bytes,
+ *   ROW_MAJOR (row stride ldb) or PRESHUFFLE_16x16 (contiguous). a_scale, b_scale: e8m0 bytes,
+ *   ROW_MAJOR ([rows, k/32], row stride given) or SHUFFLED (padded aiter layout, stride ignored).
+ * k % 64 == 0 (k % 128 == 0 is not required), n % 16 == 0.
+ */
+size_t aklr_gemm_a4w4_mxfp4_workspace_bytes(int64_t m, int64_t n, int64_t k);
+int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, const uint8_t* a_scale,
+                         int64_t lds_a, const uint8_t* b_scale, int64_t lds_b, const float* bias, void* out,
+                         int64_t ldo, int64_t m, int64_t n, int64_t k, int b_layout, int scale_layout,
+                         int out_dtype, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AKLR_AMD_H */

@@ -1,0 +1,206 @@
+"""GPU parity of the 128x128-block-scaled FP8 GEMM and the MXFP4 GEMM against the CPU oracle.
+
+Tolerance (written here, as the north star states it): |out - y| <= 1e-2 * rms(y) + 1e-2 * |y| per
+element, y the oracle's fp32 result (dequantize to fp32, then matmul); the contract's own
+ToleranceBound (atol 1e-2, rtol 1e-2 + bf16 unit roundoff) is checked too for FP8.
+Full outputs are compared up to decode sizes; prefill sizes compare a seeded sample of rows x columns
+(the oracle computes exactly those) plus size-independent properties (determinism, linearity in the
+scales).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import aklr_amd
+from aklr_amd import layouts, workloads
+from oracle import gemm as ogemm
+from oracle import quant as oquant
+from tests.helpers import bf16_bits, f32, say, u8
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _fp8_inputs(m, n, k, seed=0, dtype=torch.float8_e4m3fn):
+    x = workloads.activations(m, k, seed=seed, device=DEV)
+    q, s = aklr_amd.per_group_quant_fp8(x)
+    b, bs = workloads.blockwise_fp8_weight(n, k, seed=seed + 1, device=DEV)
+    if dtype == torch.float8_e5m2:
+        q = q.float().to(torch.float8_e5m2)
+        b = b.float().to(torch.float8_e5m2)
+    return q, s, b, bs
+
+
+def _sample(m, n, rows, cols, seed=0):
+    rng = np.random.default_rng(seed)
+    r = np.arange(m) if m <= rows else np.sort(rng.choice(m, rows, replace=False))
+    c = np.arange(n) if n <= cols else np.sort(rng.choice(n, cols, replace=False))
+    return r, c
+
+
+def _check(out, ref, what, contract=True, out_dtype="bfloat16"):
+    got = f32(out) if isinstance(out, torch.Tensor) else out
+    err, rms = ogemm.rms_normalized_error(got, ref)
+    assert ogemm.within_north_star(got, ref), f"{what}: max|err|/rms {err:.3e} outside tolerance"
+    if contract:
+        assert ogemm.within_contract_tolerance(got, ref, out_dtype), f"{what}: contract ToleranceBound exceeded"
+
+
+def _fmt(dtype):
+    return "e5m2" if dtype == torch.float8_e5m2 else "e4m3fn"
+
+
+def _run_and_check(m, n, k, *, variant="row_major", mode="K", bias=False, out_dtype=None, seed=0,
+                   dtype=torch.float8_e4m3fn, rows=64, cols=512):
+    say(f"gemm_a8w8 m={m} n={n} k={k} variant={variant} mode={mode} bias={bias} out={out_dtype} {_fmt(dtype)}")
+    q, s, b, bs = _fp8_inputs(m, n, k, seed, dtype)
+    bias_t = (torch.randn(n, device=DEV, generator=workloads.generator(seed + 7, DEV)) if bias else None)
+    kwargs = {}
+    if variant == "row_major":
+        a_scale = s.t().contiguous() if mode == "K" else s
+        bb = b
+    else:
+        bb = layouts.shuffle_weight(b)
+        kwargs["operand_format"] = "none:preshuffled"
+        if variant == "b_shuffled":
+            a_scale = s.view(m, k // 128)  # the group-major bytes, read column-major
+        else:
+            a_scale = s.t().contiguous()
+            a_scale.is_row_major = True
+    out = aklr_amd.gemm_a8w8_blockwise_scaled(q, bb, a_scale, bs, scale_major_mode=mode, bias=bias_t,
+                                              out_dtype=out_dtype, **kwargs)
+    assert isinstance(out, torch.Tensor), f"not served: {out}"
+    torch.cuda.synchronize()
+    r, c = _sample(m, n, rows, cols, seed)
+    s_np = s.cpu().numpy()  # (kb, m)
+    ref = ogemm.gemm_a8w8_blockwise_scaled(u8(q), u8(b), s_np, bs.cpu().numpy(), fmt=_fmt(dtype),
+                                           scale_major_mode="MN", bias=None if bias_t is None else f32(bias_t),
+                                           rows=r, cols=c)
+    got = f32(out)[np.ix_(r, c)]
+    _check(got, ref, f"m={m} n={n} k={k} {variant}", out_dtype="float16" if out_dtype == torch.float16 else "bfloat16")
+    return out
+
+
+def test_config1():
+    _run_and_check(32, 1024, 2048, rows=32, cols=1024)
+
+
+@pytest.mark.parametrize("nk", workloads.DEEPSEEK_NK)
+@pytest.mark.parametrize("m", workloads.DECODE_M)
+def test_decode_row_major(m, nk):
+    n, k = nk
+    _run_and_check(m, n, k, rows=128, cols=n if n * k <= 2**25 else 1024, seed=m)
+
+
+@pytest.mark.parametrize("nk", workloads.DEEPSEEK_NK)
+@pytest.mark.parametrize("m", [1, 16, 128])
+def test_decode_b_shuffled(m, nk):
+    n, k = nk
+    _run_and_check(m, n, k, variant="b_shuffled", rows=128, cols=1024, seed=m + 100)
+
+
+@pytest.mark.parametrize("nk", workloads.DEEPSEEK_NK)
+@pytest.mark.parametrize("m", workloads.PREFILL_M)
+def test_prefill_row_major(m, nk):
+    n, k = nk
+    _run_and_check(m, n, k, rows=48, cols=384, seed=m)
+
+
+@pytest.mark.parametrize("nk", workloads.DEEPSEEK_NK)
+def test_prefill_b_shuffled(nk):
+    n, k = nk
+    _run_and_check(1024, n, k, variant="b_shuffled", rows=48, cols=384, seed=3)
+
+
+@pytest.mark.parametrize("m", [5, 200])
+def test_row_major_a_scale_shuffled_b(m):
+    _run_and_check(m, 2112, 7168, variant="b_shuffled_row_major_a_scale", seed=11)
+
+
+@pytest.mark.parametrize("m", [7, 300])
+def test_mn_scales_bias_fp16(m):
+    _run_and_check(m, 2112, 1536, mode="MN", bias=True, out_dtype=torch.float16, seed=21)
+
+
+@pytest.mark.parametrize("m", [16, 256])
+def test_e5m2(m):
+    _run_and_check(m, 1024, 2048, dtype=torch.float8_e5m2, seed=31)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 128), (129, 48, 128), (17, 2112, 256), (130, 144, 384)])
+def test_small_and_ragged(m, n, k):
+    _run_and_check(m, n, k, seed=41)
+
+
+def test_out_buffer_and_determinism():
+    m, n, k = 64, 7168, 16384
+    q, s, b, bs = _fp8_inputs(m, n, k, seed=5)
+    out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+    r1 = aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s.t().contiguous(), bs, out=out)
+    assert r1 is out
+    r2 = aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s.t().contiguous(), bs)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out.float()).any()
+    assert torch.equal(r1.view(torch.int16), r2.view(torch.int16)), "decode GEMM is not bitwise reproducible"
+
+
+def test_scale_linearity():
+    # doubling every b_scale doubles the output exactly (power-of-two scaling is exact in fp32)
+    m, n, k = 2048, 2112, 1536
+    q, s, b, bs = _fp8_inputs(m, n, k, seed=6)
+    o1 = aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s.t().contiguous(), bs).float()
+    o2 = aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s.t().contiguous(), bs * 2).float()
+    torch.cuda.synchronize()
+    assert torch.equal(o1 * 2, o2)
+
+
+# ---------------------------------------------------------------------------------------------
+# MXFP4
+def _mxfp4_run(m, n, k, shuffled, seed=0, rows=64, cols=512, bias=False):
+    say(f"gemm_a4w4_mxfp4 m={m} n={n} k={k} shuffled={shuffled} bias={bias}")
+    x = workloads.activations(m, k, seed=seed, device=DEV)
+    qa, sa = aklr_amd.dynamic_mxfp4_quant(x, shuffle=shuffled)
+    qa_rm, sa_rm = aklr_amd.dynamic_mxfp4_quant(x, shuffle=False)
+    wb, sb = workloads.mxfp4_weight(n, k, seed=seed + 1, device=DEV)
+    bias_t = torch.randn(n, device=DEV, generator=workloads.generator(seed + 9, DEV)) if bias else None
+    if shuffled:
+        out = aklr_amd.gemm_a4w4_mxfp4(qa, layouts.shuffle_weight(wb), sa, layouts.e8m0_scales(sb), bias=bias_t)
+    else:
+        out = aklr_amd.gemm_a4w4_mxfp4(qa, wb, sa, sb, bias=bias_t, operand_format="none:none")
+    assert isinstance(out, torch.Tensor), f"not served: {out}"
+    torch.cuda.synchronize()
+    r, c = _sample(m, n, rows, cols, seed)
+    ref = ogemm.gemm_a4w4_mxfp4(u8(qa_rm), u8(wb), u8(sa_rm), u8(sb), bias=None if bias_t is None else f32(bias_t),
+                                rows=r, cols=c)
+    _check(f32(out)[np.ix_(r, c)], ref, f"mxfp4 m={m} n={n} k={k}", contract=False)
+    return out
+
+
+@pytest.mark.parametrize("shuffled", [True, False])
+@pytest.mark.parametrize("nk", workloads.LLAMA70B_NK)
+@pytest.mark.parametrize("m", workloads.MXFP4_M)
+def test_mxfp4_llama(m, nk, shuffled):
+    n, k = nk
+    _mxfp4_run(m, n, k, shuffled, seed=m)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 64), (3, 32, 192), (33, 48, 320), (200, 272, 64), (40, 160, 4160)])
+def test_mxfp4_small_and_ragged_k(m, n, k):
+    _mxfp4_run(m, n, k, shuffled=True, seed=m, bias=True)
+    _mxfp4_run(m, n, k, shuffled=False, seed=m + 1)
+
+
+def test_quant_gemm_pipeline_matches_oracle_end_to_end():
+    # the oracle quantizes too: activations -> codes/scales -> GEMM, all from the same bf16 input
+    m, n, k = 16, 2112, 7168
+    x = workloads.activations(m, k, seed=77, device=DEV)
+    b, bs = workloads.blockwise_fp8_weight(n, k, seed=78, device=DEV)
+    q, s = aklr_amd.per_group_quant_fp8(x)
+    out = aklr_amd.gemm_a8w8_blockwise_scaled(q, layouts.shuffle_weight(b), s.view(m, k // 128), bs,
+                                              operand_format="none:preshuffled")
+    torch.cuda.synchronize()
+    q_ref, s_ref = oquant.per_group_quant_fp8(bf16_bits(x))
+    ref = ogemm.gemm_a8w8_blockwise_scaled(q_ref, u8(b), s_ref, bs.cpu().numpy(), scale_major_mode="MN")
+    _check(out, ref, "pipeline")
