@@ -374,16 +374,24 @@ static DecodePlan plan_decode(int64_t m, int64_t n, int64_t k) {
   d.mt = m <= 16 ? 1 : m <= 32 ? 2 : m <= 64 ? 4 : 8;
   d.nt = 1;
   const int KB = (int)(k / 128);
-  d.nw = (d.mt == 8 || KB < 16) ? 4 : 8;
-  const int64_t n_tiles = (n + 16 * d.nt - 1) / (16 * d.nt);
-  // Aim at >= 4096 waves in flight (16 per CU); keep at least 2 K blocks per wave, and keep the
-  // fp32 partial traffic (8 bytes per output per split) under ~15% of the weight bytes.
-  int64_t s = (4096 + n_tiles * d.nw - 1) / (n_tiles * d.nw);
-  int64_t s_max = KB / (2 * d.nw);
-  const int64_t s_traffic = (int64_t)(0.15 * (double)k / (8.0 * (double)m));
-  if (s_traffic < s_max) s_max = s_traffic;
-  if (s > s_max) s = s_max;
-  if (s < 1) s = 1;
+  const int64_t n_tiles = (n + 15) / 16;
+  // Waves per workgroup: double until ~2048 waves cover the weight (8 per CU), each wave keeping
+  // at least 2 K blocks; register and LDS budgets cap it by MT.
+  const int nw_max = d.mt <= 2 ? 16 : d.mt == 4 ? 8 : 4;
+  d.nw = 4;
+  while (d.nw * 2 <= nw_max && n_tiles * d.nw < 2048 && KB >= 4 * d.nw) d.nw *= 2;
+  // Split K across workgroups only when the columns alone give too few waves, keeping at least
+  // 2 K blocks per wave and the fp32 partial traffic (8 bytes per output per split) under ~15% of
+  // the weight bytes.
+  int64_t s = 1;
+  if (n_tiles * d.nw < 1024) {
+    s = (2048 + n_tiles * d.nw - 1) / (n_tiles * d.nw);
+    int64_t s_max = KB / (2 * d.nw);
+    const int64_t s_traffic = (int64_t)(0.15 * (double)k / (8.0 * (double)m));
+    if (s_traffic < s_max) s_max = s_traffic;
+    if (s > s_max) s = s_max;
+    if (s < 1) s = 1;
+  }
   d.kb_per_split = (int)((KB + s - 1) / s);
   d.splits = (int)((KB + d.kb_per_split - 1) / d.kb_per_split);
   return d;
@@ -397,8 +405,10 @@ static void launch_decode(const Gemm8Args& a, const DecodePlan& d, hipStream_t s
 
 template <int FMT, bool PRE>
 static int dispatch_decode(const Gemm8Args& a, const DecodePlan& d, hipStream_t s) {
-  if (d.mt == 1 && d.nw == 8) launch_decode<1, 1, 8, FMT, PRE>(a, d, s);
+  if (d.mt == 1 && d.nw == 16) launch_decode<1, 1, 16, FMT, PRE>(a, d, s);
+  else if (d.mt == 1 && d.nw == 8) launch_decode<1, 1, 8, FMT, PRE>(a, d, s);
   else if (d.mt == 1) launch_decode<1, 1, 4, FMT, PRE>(a, d, s);
+  else if (d.mt == 2 && d.nw == 16) launch_decode<2, 1, 16, FMT, PRE>(a, d, s);
   else if (d.mt == 2 && d.nw == 8) launch_decode<2, 1, 8, FMT, PRE>(a, d, s);
   else if (d.mt == 2) launch_decode<2, 1, 4, FMT, PRE>(a, d, s);
   else if (d.mt == 4 && d.nw == 8) launch_decode<4, 1, 8, FMT, PRE>(a, d, s);

@@ -1,0 +1,318 @@
+"""Benchmark of the block-scaled FP8 GEMM path on one MI355X.
+
+Workload (the config the metric's decode figure is quoted on): DeepSeek-V3
+decode FP8 block-scaled GEMM, M in {1, 4, 16, 64, 128} x (N, K) in {(2112, 7168), (24576, 1536),
+(7168, 16384)}. One step = for each of the 15 (M, N, K): per_group_quant_fp8 of the bf16 activations
+(N(0,1), 1% x20 outliers) then the 128x128-block-scaled GEMM against e4m3 weights (N(0,0.02), 128x128
+fp32 block scales) in aiter's preshuffled layout with the quantizer's column-major scales, bf16 out.
+Each step is one HIP graph; steps rotate over enough weight copies (> 512 MB per shape) that the
+256 MB MALL holds none of them, so weights stream from HBM as in serving.
+
+value = whole-step algorithmic bytes / step time, in GB/s (bytes per GEMM: M*K + 4*M*K/128 + N*K +
+4*ceil(N/128)*K/128 + 2*M*N; per quant: 3.03125*M*K).
+roofline: the dominant kernel, the decode GEMM at M=16, (N, K) = (7168, 16384) (117.97 MB per launch),
+timed alone with HIP events on its stream over graph replays; peak 8 TB/s.
+prefill / mxfp4: extra figures (TFLOP/s vs the dense FP8 5.0 PF / MXFP4 10.1 PF peaks) at M=4096.
+cpu_baseline: the CPU oracle (numpy dequantize + fp32 matmul, the reference check's formula) on a
+bounded sample (decode M=16, the three shapes), timed on the host in the same run.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+MXFP4_PEAK_TFLOPS = 10100.0
+
+
+def gemm8_bytes(m, n, k):
+    return m * k + 4 * m * k // 128 + n * k + 4 * (-(-n // 128)) * (k // 128) + 2 * m * n
+
+
+def quant8_bytes(m, k):
+    return 2 * m * k + m * k + 4 * m * k // 128
+
+
+def gemm4_bytes(m, n, k):
+    return (m + n) * k // 2 + (m + n) * k // 32 + 2 * m * n
+
+
+def _copies(bytes_per_copy, target=512 * 2**20, lo=2):
+    return max(lo, math.ceil(target / bytes_per_copy))
+
+
+def _replay_time_ms(graphs, steps, warmup, stream):
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def _capture(fn, stream):
+    fn()  # eager run first: any lazy init happens outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    return g
+
+
+def build_decode(dev, shuffled=True):
+    import aklr_amd
+    from aklr_amd import layouts, workloads
+
+    shapes = workloads.DEEPSEEK_NK
+    ms = workloads.DECODE_M
+    weights = {}
+    for (n, k) in shapes:
+        per = gemm8_bytes(0, n, k)
+        copies = []
+        for r in range(_copies(per, lo=4)):
+            b, bs = workloads.blockwise_fp8_weight(n, k, seed=100 + r, device=dev)
+            copies.append((layouts.shuffle_weight(b) if shuffled else b, bs))
+        weights[(n, k)] = copies
+    xs = {(m, k): workloads.activations(m, k, seed=m * 7 + k, device=dev) for m in ms for (_, k) in shapes}
+    n_sets = max(len(c) for c in weights.values())
+
+    def step_fn(r):
+        def run():
+            for (n, k) in shapes:
+                b, bs = weights[(n, k)][r % len(weights[(n, k)])]
+                for m in ms:
+                    q, s = aklr_amd.per_group_quant_fp8(xs[(m, k)])
+                    if shuffled:
+                        aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s.view(m, k // 128), bs,
+                                                            operand_format="none:preshuffled")
+                    else:
+                        aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s, bs, scale_major_mode="MN")
+        return run
+
+    step_bytes = sum(gemm8_bytes(m, n, k) + quant8_bytes(m, k) for (n, k) in shapes for m in ms)
+    return step_fn, n_sets, step_bytes, weights, xs
+
+
+def time_gemm8(dev, m, n, k, weights, steps, stream, shuffled=True, calls_per_graph=None):
+    """Average duration of one GEMM launch (all kernels of the op) at (m, n, k), rotating over the
+    weight copies inside one graph, from HIP events on the launch stream."""
+    import aklr_amd
+    from aklr_amd import workloads
+
+    x = workloads.activations(m, k, seed=5, device=dev)
+    q, s = aklr_amd.per_group_quant_fp8(x)
+    copies = weights[(n, k)]
+    calls = calls_per_graph or len(copies)
+
+    def run():
+        for i in range(calls):
+            b, bs = copies[i % len(copies)]
+            if shuffled:
+                aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s.view(m, k // 128), bs, operand_format="none:preshuffled")
+            else:
+                aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s, bs, scale_major_mode="MN")
+
+    g = _capture(run, stream)
+    ms = _replay_time_ms([g], steps, 2, stream)
+    return ms / calls
+
+
+def prefill_figures(dev, stream, steps=10):
+    import aklr_amd
+    from aklr_amd import layouts, workloads
+
+    out = []
+    m = 4096
+    for (n, k) in workloads.DEEPSEEK_NK:
+        x = workloads.activations(m, k, seed=1, device=dev)
+        q, s = aklr_amd.per_group_quant_fp8(x)
+        b, bs = workloads.blockwise_fp8_weight(n, k, seed=2, device=dev)
+        bsh = layouts.shuffle_weight(b)
+        g = _capture(lambda: aklr_amd.gemm_a8w8_blockwise_scaled(q, bsh, s.view(m, k // 128), bs,
+                                                                 operand_format="none:preshuffled"), stream)
+        t = _replay_time_ms([g], steps, 2, stream)
+        tf = 2.0 * m * n * k / (t * 1e-3) / 1e12
+        out.append({"m": m, "n": n, "k": k, "us": round(t * 1e3, 2), "tflops": round(tf, 1),
+                    "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)})
+    return out
+
+
+def mxfp4_figures(dev, stream, steps=10):
+    import aklr_amd
+    from aklr_amd import layouts, workloads
+
+    out = []
+    for m in (1, 4096):
+        for (n, k) in workloads.LLAMA70B_NK:
+            x = workloads.activations(m, k, seed=1, device=dev)
+            qa, sa = aklr_amd.dynamic_mxfp4_quant(x, shuffle=True)
+            per = gemm4_bytes(0, n, k)
+            copies = []
+            for r in range(_copies(per, lo=2) if m == 1 else 1):
+                wb, sb = workloads.mxfp4_weight(n, k, seed=10 + r, device=dev)
+                copies.append((layouts.shuffle_weight(wb), layouts.e8m0_scales(sb)))
+
+            def run(copies=copies, qa=qa, sa=sa):
+                for wb, sb in copies:
+                    aklr_amd.gemm_a4w4_mxfp4(qa, wb, sa, sb)
+
+            g = _capture(run, stream)
+            t = _replay_time_ms([g], steps, 2, stream) / len(copies)
+            rec = {"m": m, "n": n, "k": k, "us": round(t * 1e3, 2)}
+            if m == 1:
+                gbs = gemm4_bytes(m, n, k) / (t * 1e-3) / 1e9
+                rec.update(gbs=round(gbs, 1), frac_hbm_peak=round(gbs / HBM_PEAK_GBS, 4))
+            else:
+                tf = 2.0 * m * n * k / (t * 1e-3) / 1e12
+                rec.update(tflops=round(tf, 1), frac_mxfp4_peak=round(tf / MXFP4_PEAK_TFLOPS, 4))
+            out.append(rec)
+            del copies
+    return out
+
+
+def cpu_baseline():
+    """The CPU oracle on decode M=16 over the three DeepSeek shapes (quantize + dequantize + fp32
+    matmul), one timed repetition after a warm-up of the smallest shape."""
+    import numpy as np
+
+    from aklr_amd import workloads
+    from oracle import gemm as ogemm
+    from oracle import quant as oquant
+
+    m = 16
+    cases = []
+    for (n, k) in workloads.DEEPSEEK_NK:
+        x = workloads.activations(m, k, seed=3, device="cpu")
+        b, bs = workloads.blockwise_fp8_weight(n, k, seed=4, device="cpu")
+        cases.append((x.view(torch.int16).numpy().view(np.uint16), b.view(torch.uint8).numpy(), bs.numpy(), n, k))
+    xb, b, bs, n, k = cases[0]
+    q, s = oquant.per_group_quant_fp8(xb)
+    ogemm.gemm_a8w8_blockwise_scaled(q, b, s, bs, scale_major_mode="MN")
+    total_bytes = 0
+    t0 = time.perf_counter()
+    for xb, b, bs, n, k in cases:
+        q, s = oquant.per_group_quant_fp8(xb)
+        ogemm.gemm_a8w8_blockwise_scaled(q, b, s, bs, scale_major_mode="MN")
+        total_bytes += gemm8_bytes(m, n, k) + quant8_bytes(m, k)
+    dt = time.perf_counter() - t0
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        cores = os.cpu_count() or 1
+    return {
+        "value": round(total_bytes / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": int(cores),
+        "kind": "port",
+        "sample": f"decode M=16 x (N,K) in (2112,7168),(24576,1536),(7168,16384): quant + dequant + fp32 "
+                  f"matmul, 1 rep, {dt:.2f} s",
+    }
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layout", choices=("preshuffled", "row_major"), default="preshuffled")
+    ap.add_argument("--no-extras", action="store_true", help="skip the prefill/MXFP4 figures")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        return 2
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    # graphs are captured on (and every launch and event goes to) one non-default stream of
+    # default priority
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.set_stream(stream)
+    shuffled = args.layout == "preshuffled"
+    print(f"[bench] building decode workload ({args.layout})", file=sys.stderr, flush=True)
+    step_fn, n_sets, step_bytes, weights, _ = build_decode(dev, shuffled)
+    graphs = [_capture(step_fn(r), stream) for r in range(n_sets)]
+    print(f"[bench] {len(graphs)} step graphs captured; timing {args.steps} steps", file=sys.stderr, flush=True)
+    ms_per_step = _replay_time_ms(graphs, args.steps, args.warmup, stream)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    m_dom, n_dom, k_dom = 16, 7168, 16384
+    t_dom = time_gemm8(dev, m_dom, n_dom, k_dom, weights, max(10, args.steps), stream, shuffled)
+    dom_bytes = gemm8_bytes(m_dom, n_dom, k_dom)
+    achieved = dom_bytes / (t_dom * 1e-3) / 1e9
+    per_shape = []
+    for (n, k) in ((2112, 7168), (24576, 1536), (7168, 16384)):
+        for m in (1, 16, 128):
+            t = time_gemm8(dev, m, n, k, weights, 10, stream, shuffled)
+            per_shape.append({"m": m, "n": n, "k": k, "us": round(t * 1e3, 2),
+                              "gbs": round(gemm8_bytes(m, n, k) / (t * 1e-3) / 1e9, 1)})
+    del graphs, weights
+    torch.cuda.empty_cache()
+
+    extras = {}
+    if not args.no_extras:
+        print("[bench] prefill and MXFP4 figures", file=sys.stderr, flush=True)
+        extras["prefill_fp8_m4096"] = prefill_figures(dev, stream)
+        torch.cuda.empty_cache()
+        extras["mxfp4"] = mxfp4_figures(dev, stream)
+        torch.cuda.empty_cache()
+    cpu = None
+    if not args.no_cpu:
+        print("[bench] CPU baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline()
+
+    line = {
+        "metric": "block-scaled FP8 GEMM decode HBM GB/s (DeepSeek-V3 decode config)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3",
+        "data": "synthetic (seeded N(0,1) activations with 1% x20 outliers, N(0,0.02) weights)",
+        "config": {
+            "workload": "deepseek_v3_decode_fp8_blockscale: M in {1,4,16,64,128} x (N,K) in "
+                        "{(2112,7168),(24576,1536),(7168,16384)}, quant + GEMM per step",
+            "b_layout": args.layout,
+            "weight_copies_rotated": n_sets,
+            "step_bytes": step_bytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"gemm8_decode_kernel (M={m_dom}, N={n_dom}, K={k_dom})",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "launch_us": round(t_dom * 1e3, 2),
+            "bytes_per_launch": dom_bytes,
+        },
+        "decode_per_shape": per_shape,
+        **extras,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
