@@ -236,8 +236,10 @@ __global__ __launch_bounds__(256) void gemm8_tile_kernel(Gemm8Args p) {
 
   const int tiles_m = (p.m + kTileM - 1) / kTileM;
   const int tiles_n = (p.n + kTileN - 1) / kTileN;
-  // XCD-aware order, then groups of 8 tile-rows so neighbouring tiles share A rows and B columns.
-  const int pid = (int)xcd_remap(blockIdx.x, gridDim.x);
+  // XCD-aware order (the K splits of one tile are consecutive, so they share an XCD and its L2),
+  // then groups of 8 tile-rows so neighbouring tiles share A rows and B columns.
+  const int lid = (int)xcd_remap(blockIdx.x, gridDim.x);
+  const int pid = lid / p.splits, split = lid % p.splits;
   constexpr int kGroup = 8;
   const int per_group = kGroup * tiles_n;
   const int group = pid / per_group;
@@ -251,7 +253,8 @@ __global__ __launch_bounds__(256) void gemm8_tile_kernel(Gemm8Args p) {
   const int lane = t & 63, w = t >> 6;
   const int li = lane & 15, g = lane >> 4;
   const int wm = w >> 1, wn = w & 1;
-  const int KB = p.k >> 7;
+  const int kb_begin = split * p.kb_per_split;
+  const int kb_end = min(p.k >> 7, kb_begin + p.kb_per_split);
   const int64_t kt32 = p.k >> 5;
 
   // global -> register staging
@@ -311,12 +314,12 @@ __global__ __launch_bounds__(256) void gemm8_tile_kernel(Gemm8Args p) {
 
   const float* sbrow = p.sb + (int64_t)(n0 >> 7) * p.ldbs;
 
-  gload(0);
+  gload(kb_begin);
   lstore(0);
   __syncthreads();
-  for (int kb = 0; kb < KB; ++kb) {
-    const int st = kb & 1;
-    if (kb + 1 < KB) gload(kb + 1);
+  for (int kb = kb_begin; kb < kb_end; ++kb) {
+    const int st = (kb - kb_begin) & 1;
+    if (kb + 1 < kb_end) gload(kb + 1);
     const float sb = sbrow[kb];
     i32x8 bf[4];
 #pragma unroll
@@ -344,7 +347,7 @@ __global__ __launch_bounds__(256) void gemm8_tile_kernel(Gemm8Args p) {
         for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(part[r], s4[r], acc[mt][nt][r]);
       }
     }
-    if (kb + 1 < KB) lstore(st ^ 1);
+    if (kb + 1 < kb_end) lstore(st ^ 1);
     __syncthreads();
   }
 
@@ -354,6 +357,14 @@ __global__ __launch_bounds__(256) void gemm8_tile_kernel(Gemm8Args p) {
     for (int nt = 0; nt < 4; ++nt) {
       const int col = n0 + wn * 64 + nt * 16 + li;
       if (col >= p.n) continue;
+      if (p.splits > 1) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + wm * 64 + mt * 16 + 4 * g + r;
+          if (row < p.m) p.partial[((int64_t)split * p.m + row) * p.n + col] = acc[mt][nt][r];
+        }
+        continue;
+      }
       const float bv = p.bias ? p.bias[col] : 0.0f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -365,21 +376,23 @@ __global__ __launch_bounds__(256) void gemm8_tile_kernel(Gemm8Args p) {
 
 // ---------------------------------------------------------------------------------------------
 // host-side planning
+
+// m <= kDecodeMaxM streams the weight through the decode kernel; larger m runs the MFMA tile kernel.
+static constexpr int64_t kDecodeMaxM = 32;
+
 struct DecodePlan {
-  int mt, nt, nw, splits, kb_per_split;
+  int mt, nw, splits, kb_per_split;
 };
 
 static DecodePlan plan_decode(int64_t m, int64_t n, int64_t k) {
   DecodePlan d;
-  d.mt = m <= 16 ? 1 : m <= 32 ? 2 : m <= 64 ? 4 : 8;
-  d.nt = 1;
+  d.mt = m <= 16 ? 1 : 2;
   const int KB = (int)(k / 128);
   const int64_t n_tiles = (n + 15) / 16;
   // Waves per workgroup: double until ~2048 waves cover the weight (8 per CU), each wave keeping
-  // at least 2 K blocks; register and LDS budgets cap it by MT.
-  const int nw_max = d.mt <= 2 ? 16 : d.mt == 4 ? 8 : 4;
+  // at least 2 K blocks.
   d.nw = 4;
-  while (d.nw * 2 <= nw_max && n_tiles * d.nw < 2048 && KB >= 4 * d.nw) d.nw *= 2;
+  while (d.nw < 16 && n_tiles * d.nw < 2048 && KB >= 4 * d.nw) d.nw *= 2;
   // Split K across workgroups only when the columns alone give too few waves, keeping at least
   // 2 K blocks per wave and the fp32 partial traffic (8 bytes per output per split) under ~15% of
   // the weight bytes.
@@ -397,42 +410,78 @@ static DecodePlan plan_decode(int64_t m, int64_t n, int64_t k) {
   return d;
 }
 
-template <int MT, int NT, int NW, int FMT, bool PRE>
+struct TilePlan {
+  int tiles, splits, kb_per_split;
+};
+
+static TilePlan plan_tile(int64_t m, int64_t n, int64_t k) {
+  TilePlan t;
+  t.tiles = (int)(((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN));
+  const int KB = (int)(k / 128);
+  // Split K when the tiles alone leave CUs idle: aim at 2 workgroups per CU (512), keep at least 4
+  // K blocks per split, and keep the fp32 partials (8 bytes per output per split, written then
+  // summed) within the weight's own bytes.
+  int64_t s = 1;
+  if (t.tiles < 512) {
+    s = (512 + t.tiles - 1) / t.tiles;
+    int64_t s_max = KB / 4;
+    const int64_t s_traffic = k / (8 * m);
+    if (s_traffic < s_max) s_max = s_traffic;
+    if (s > s_max) s = s_max;
+    if (s < 1) s = 1;
+  }
+  t.kb_per_split = (int)((KB + s - 1) / s);
+  t.splits = (int)((KB + t.kb_per_split - 1) / t.kb_per_split);
+  return t;
+}
+
+template <int MT, int NW, int FMT, bool PRE>
 static void launch_decode(const Gemm8Args& a, const DecodePlan& d, hipStream_t s) {
-  dim3 grid((unsigned)((a.n + 16 * NT - 1) / (16 * NT)), (unsigned)d.splits);
-  hipLaunchKernelGGL((gemm8_decode_kernel<MT, NT, NW, FMT, PRE>), grid, dim3(NW * 64), 0, s, a);
+  dim3 grid((unsigned)((a.n + 15) / 16), (unsigned)d.splits);
+  hipLaunchKernelGGL((gemm8_decode_kernel<MT, 1, NW, FMT, PRE>), grid, dim3(NW * 64), 0, s, a);
 }
 
 template <int FMT, bool PRE>
-static int dispatch_decode(const Gemm8Args& a, const DecodePlan& d, hipStream_t s) {
-  if (d.mt == 1 && d.nw == 16) launch_decode<1, 1, 16, FMT, PRE>(a, d, s);
-  else if (d.mt == 1 && d.nw == 8) launch_decode<1, 1, 8, FMT, PRE>(a, d, s);
-  else if (d.mt == 1) launch_decode<1, 1, 4, FMT, PRE>(a, d, s);
-  else if (d.mt == 2 && d.nw == 16) launch_decode<2, 1, 16, FMT, PRE>(a, d, s);
-  else if (d.mt == 2 && d.nw == 8) launch_decode<2, 1, 8, FMT, PRE>(a, d, s);
-  else if (d.mt == 2) launch_decode<2, 1, 4, FMT, PRE>(a, d, s);
-  else if (d.mt == 4 && d.nw == 8) launch_decode<4, 1, 8, FMT, PRE>(a, d, s);
-  else if (d.mt == 4) launch_decode<4, 1, 4, FMT, PRE>(a, d, s);
-  else launch_decode<8, 1, 4, FMT, PRE>(a, d, s);
-  return AKLR_OK;
+static void dispatch_decode(const Gemm8Args& a, const DecodePlan& d, hipStream_t s) {
+  if (d.mt == 1) {
+    if (d.nw == 16) launch_decode<1, 16, FMT, PRE>(a, d, s);
+    else if (d.nw == 8) launch_decode<1, 8, FMT, PRE>(a, d, s);
+    else launch_decode<1, 4, FMT, PRE>(a, d, s);
+  } else {
+    if (d.nw == 16) launch_decode<2, 16, FMT, PRE>(a, d, s);
+    else if (d.nw == 8) launch_decode<2, 8, FMT, PRE>(a, d, s);
+    else launch_decode<2, 4, FMT, PRE>(a, d, s);
+  }
 }
 
 template <int FMT, bool PRE>
-static void launch_tile(const Gemm8Args& a, hipStream_t s) {
-  const int tiles = ((a.m + kTileM - 1) / kTileM) * ((a.n + kTileN - 1) / kTileN);
-  hipLaunchKernelGGL((gemm8_tile_kernel<FMT, PRE>), dim3((unsigned)tiles), dim3(256), 0, s, a);
+static void launch_tile(const Gemm8Args& a, const TilePlan& t, hipStream_t s) {
+  hipLaunchKernelGGL((gemm8_tile_kernel<FMT, PRE>), dim3((unsigned)(t.tiles * t.splits)), dim3(256), 0, s, a);
 }
 
-static constexpr int64_t kDecodeMaxM = 128;
+// Splits and K blocks per split of the kernel that will serve (m, n, k); returns the workspace
+// bytes it needs (fp32 partials [splits, m, n] when splits > 1).
+static size_t plan_splits(int64_t m, int64_t n, int64_t k, int* splits, int* kb_per_split) {
+  if (m <= kDecodeMaxM) {
+    const DecodePlan d = plan_decode(m, n, k);
+    *splits = d.splits;
+    *kb_per_split = d.kb_per_split;
+  } else {
+    const TilePlan t = plan_tile(m, n, k);
+    *splits = t.splits;
+    *kb_per_split = t.kb_per_split;
+  }
+  return *splits > 1 ? (size_t)*splits * (size_t)m * (size_t)n * sizeof(float) : 0;
+}
 
 }  // namespace aklr
 
 using namespace aklr;
 
 extern "C" size_t aklr_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k) {
-  if (m <= 0 || n <= 0 || k < 128 || m > kDecodeMaxM) return 0;
-  const DecodePlan d = plan_decode(m, n, k);
-  return d.splits > 1 ? (size_t)d.splits * (size_t)m * (size_t)n * sizeof(float) : 0;
+  if (m <= 0 || n <= 0 || k < 128) return 0;
+  int splits, kps;
+  return plan_splits(m, n, k, &splits, &kps);
 }
 
 extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void* b, int64_t ldb,
@@ -474,33 +523,32 @@ extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void*
   g.k = (int)k;
   g.out_dtype = out_dtype;
   g.partial = nullptr;
-  g.splits = 1;
-  g.kb_per_split = (int)(k / 128);
   const bool pre = b_layout == AKLR_B_PRESHUFFLE_16x16;
   const bool e5 = fp8_dtype == AKLR_FP8_E5M2;
 
+  int splits, kps;
+  const size_t need = plan_splits(m, n, k, &splits, &kps);
+  g.splits = splits;
+  g.kb_per_split = kps;
+  if (splits > 1) {
+    if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) return AKLR_ERR_WORKSPACE;
+    g.partial = static_cast<float*>(workspace);
+  }
   if (m <= kDecodeMaxM) {
     const DecodePlan d = plan_decode(m, n, k);
-    g.splits = d.splits;
-    g.kb_per_split = d.kb_per_split;
-    if (d.splits > 1) {
-      const size_t need = (size_t)d.splits * (size_t)m * (size_t)n * sizeof(float);
-      if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) return AKLR_ERR_WORKSPACE;
-      g.partial = static_cast<float*>(workspace);
-    }
     if (e5) pre ? dispatch_decode<1, true>(g, d, stream) : dispatch_decode<1, false>(g, d, stream);
     else pre ? dispatch_decode<0, true>(g, d, stream) : dispatch_decode<0, false>(g, d, stream);
-    AKLR_LAUNCH_CHECK();
-    if (d.splits > 1) {
-      const int64_t quads = (m * n) / 4;
-      hipLaunchKernelGGL(gemm8_splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
-                         g.partial, d.splits, g.m, g.n, bias, out, ldo, out_dtype);
-      AKLR_LAUNCH_CHECK();
-    }
-    return AKLR_OK;
+  } else {
+    const TilePlan t = plan_tile(m, n, k);
+    if (e5) pre ? launch_tile<1, true>(g, t, stream) : launch_tile<1, false>(g, t, stream);
+    else pre ? launch_tile<0, true>(g, t, stream) : launch_tile<0, false>(g, t, stream);
   }
-  if (e5) pre ? launch_tile<1, true>(g, stream) : launch_tile<1, false>(g, stream);
-  else pre ? launch_tile<0, true>(g, stream) : launch_tile<0, false>(g, stream);
   AKLR_LAUNCH_CHECK();
+  if (splits > 1) {
+    const int64_t quads = (m * n) / 4;
+    hipLaunchKernelGGL(gemm8_splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
+                       g.partial, splits, g.m, g.n, bias, out, ldo, out_dtype);
+    AKLR_LAUNCH_CHECK();
+  }
   return AKLR_OK;
 }

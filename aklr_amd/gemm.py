@@ -183,7 +183,7 @@ def gemm_a8w8_blockwise_scaled(
     if not trans_b:
         return FallbackReason.NO_WORKLOAD
     b_layout = _lib.B_ROW_MAJOR if variant == "row_major" else _lib.B_PRESHUFFLE_16x16
-    path = "decode" if m <= 128 else "tile"
+    path = "decode" if m <= 32 else "tile"  # the library picks the same way (kDecodeMaxM)
     return _Gemm8Plan(a, b, a_scale, b_scale, bias, out, dt, m, n, k, sa_sm, sa_sk, b_layout, variant,
                       f"aklr_gemm_a8w8_blockscale:{path}")
 
