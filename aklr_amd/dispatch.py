@@ -7,10 +7,12 @@ Mirrors aklr/core/runtime/dispatch/_dispatcher.py:
 - ``api.serving(...)`` answers the same question without running anything: the ``KernelInfo`` of the
   kernel that would serve the call, or the reason (:248-263); ``api.fallback_reason(...)`` is ``None``
   or the reason (:242-246);
-- ``AKLR_DISABLE`` (comma-separated contract ids or op names, or ``all``) closes ops with
-  ``FallbackReason.DISABLED`` (aklr/core/platform/env.py:53-104);
-- ``AKLR_TRACE=op|all`` logs each distinct (op, variant, outcome) once per process
-  (aklr/core/runtime/dispatch/_trace.py:36-100).
+- ``AKLR_DISABLE``: ``"1"`` closes every op, ``"0"`` or unset none, anything else is a
+  comma-separated list of contract ids (``per_group_quant_fp8@1.0``) to close; a closed op returns
+  ``FallbackReason.DISABLED`` (aklr/core/platform/env.py:59-64);
+- ``AKLR_TRACE``: ``"0"``/unset, ``"plugin"``, ``"op"`` or ``"all"`` (any other value raises
+  ``ValueError``, env.py:44-50); ``op``/``all`` log each distinct (op, variant, outcome) once per
+  process (aklr/core/runtime/dispatch/_trace.py:36-100).
 
 What differs by design: there is no per-shape dispatch table. Every in-contract call that reaches a
 supported layout is served by the compiled HIP kernels, which need no warm-up (nothing compiles at
@@ -54,15 +56,34 @@ class KernelInfo:
 
 ENV_DISABLE = "AKLR_DISABLE"
 ENV_TRACE = "AKLR_TRACE"
+ENV_AITER_PLUGIN = "AKLR_AITER_PLUGIN"
+
+
+def all_disabled() -> bool:
+    return (os.environ.get(ENV_DISABLE) or "0") == "1"
 
 
 def disabled(contract_id: str) -> bool:
-    value = os.environ.get(ENV_DISABLE, "").strip()
-    if not value:
+    value = os.environ.get(ENV_DISABLE) or "0"
+    if value == "1":
+        return True
+    if value == "0":
         return False
-    names = {v.strip() for v in value.split(",") if v.strip()}
-    op = contract_id.split("@", 1)[0]
-    return "all" in names or contract_id in names or op in names
+    return contract_id in {item.strip() for item in value.split(",")}
+
+
+def trace_mode() -> str:
+    mode = os.environ.get(ENV_TRACE) or "0"
+    if mode not in ("0", "plugin", "op", "all"):
+        raise ValueError(f"{ENV_TRACE}={mode!r}: expected '0', 'plugin', 'op' or 'all'")
+    return mode
+
+
+def aiter_plugin_enabled() -> bool:
+    value = os.environ.get(ENV_AITER_PLUGIN) or "0"
+    if value not in ("0", "1"):
+        raise ValueError(f"{ENV_AITER_PLUGIN}={value!r}: expected '1' or '0'")
+    return value == "1"
 
 
 _trace_seen: set = set()
@@ -70,8 +91,7 @@ _trace_lock = threading.Lock()
 
 
 def trace(contract_id: str, variant: str | None, outcome) -> None:
-    mode = os.environ.get(ENV_TRACE, "").strip()
-    if mode not in ("op", "all"):
+    if trace_mode() not in ("op", "all"):
         return
     key = (contract_id, variant, str(outcome))
     with _trace_lock:
@@ -134,6 +154,7 @@ def api(contract_id: str, run_fn):
 
     def bind(plan_fn):
         def _plan(*args, **kwargs):
+            trace_mode()  # a bad AKLR_TRACE raises on every call, as the reference's RuntimeEnv() does
             if disabled(contract_id):
                 return FallbackReason.DISABLED
             return plan_fn(*args, **kwargs)

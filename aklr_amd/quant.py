@@ -18,7 +18,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .dispatch import FallbackReason, aligned, api
+from .dispatch import FallbackReason, aligned, api, on_gpu
 
 _MAX_TOKENS = 131072
 _MAX_HIDDEN = 21504
@@ -35,7 +35,7 @@ def _stream(device) -> int:
 def _x_ok(x, multiple: int, max_hidden: int = _MAX_HIDDEN):
     if not isinstance(x, torch.Tensor) or x.dim() != 2 or x.dtype != torch.bfloat16:
         return False
-    if x.device.type != "cuda" or not x.is_contiguous() or not aligned(x):
+    if not on_gpu(x) or not x.is_contiguous() or not aligned(x):
         return False
     t, h = x.shape
     return 1 <= t <= _MAX_TOKENS and multiple <= h <= max_hidden and h % multiple == 0

@@ -91,7 +91,7 @@ def f32_to_e4m3fn(x: np.ndarray) -> np.ndarray:
     lsb = (a >> 20) & 1
     rounded = (a.astype(np.int64) + 0x7FFFF + lsb) >> 20  # (exponent << 3) | 3 fraction bits
     normal = rounded - (120 << 3)
-    sub = np.rint(np.abs(x) * np.float32(512.0)).astype(np.int64)
+    sub = np.rint(np.minimum(np.abs(x), np.float32(1.0)) * np.float32(512.0)).astype(np.int64)  # used below 2**-6 only
     code = np.where(a < np.uint32(0x3C800000), sub, normal)  # 0x3C800000 = 2**-6
     code = np.where((code > 0x7E) | (a > np.uint32(0x7F800000)), 0x7F, code)
     return (code.astype(np.uint8) | sign).astype(np.uint8)
@@ -143,5 +143,5 @@ def fp4x2_to_f32(packed: np.ndarray) -> np.ndarray:
 
 def e8m0_to_f32(codes: np.ndarray) -> np.ndarray:
     codes = np.asarray(codes, dtype=np.uint8)
-    v = np.ldexp(np.float32(1.0), codes.astype(np.int32) - 127).astype(np.float32)
+    v = np.ldexp(np.float32(1.0), np.minimum(codes, 254).astype(np.int32) - 127).astype(np.float32)
     return np.where(codes == 255, np.float32(np.nan), v).astype(np.float32)

@@ -38,3 +38,13 @@ def _aklr_env(monkeypatch):
         if name.startswith("AKLR_"):
             monkeypatch.delenv(name, raising=False)
     yield
+
+
+@pytest.fixture(scope="session")
+def native_lib():
+    """The built C-ABI library (built here when missing; loading needs no GPU)."""
+    from aklr_amd import _build, _lib
+
+    if not _build.LIB_PATH.exists():
+        _build.build()
+    return _lib.lib()

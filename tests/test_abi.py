@@ -1,0 +1,77 @@
+"""The C-ABI library without a GPU: it loads, exports every entry point include/aklr_amd.h declares
+(unmangled), matches the Python binding's table, and rejects invalid arguments before any launch."""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+from aklr_amd import _build, _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "aklr_amd.h"
+
+
+def declared() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(aklr_\w+)\s*\(", text))
+
+
+def test_header_declares_the_binding_table():
+    assert declared() == set(_lib.SIGNATURES)
+
+
+def test_every_declared_symbol_is_exported(native_lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_build.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = declared() - exported
+    assert not missing, f"not exported (or C++-mangled): {sorted(missing)}"
+    for name in declared():
+        assert hasattr(native_lib, name)
+
+
+def test_version_and_status_strings(native_lib):
+    assert native_lib.aklr_abi_version() == _lib.ABI_VERSION
+    assert native_lib.aklr_status_string(0) == b"ok"
+    assert native_lib.aklr_status_string(1) == b"invalid argument"
+    assert native_lib.aklr_status_string(3) == b"workspace too small"
+    assert native_lib.aklr_status_string(99) == b"unknown status"
+
+
+def test_invalid_arguments_rejected_before_launch(native_lib):
+    L = native_lib
+    buf = ctypes.create_string_buffer(1 << 16)
+    p = ctypes.addressof(buf)
+    p16 = (p + 15) & ~15
+    # null pointers
+    assert L.aklr_per_group_quant_fp8(None, 128, p16, p16, 1, 128, None) == 1
+    # hidden size not a multiple of 128 / 32
+    assert L.aklr_per_group_quant_fp8(p16, 100, p16, p16, 1, 100, None) == 1
+    assert L.aklr_per_group_quant_mxfp8(p16, 48, p16, p16, 1, 48, None) == 1
+    assert L.aklr_dynamic_mxfp4_quant(p16, 64, p16, p16, 1, 64, 7, None) == 2  # unknown scale layout
+    # misaligned x
+    assert L.aklr_per_group_quant_fp8(p16 + 2, 128, p16, p16, 1, 128, None) == 1
+    # zero tokens: nothing to launch
+    assert L.aklr_per_group_quant_fp8(p16, 128, p16, p16, 0, 128, None) == 0
+    # GEMM: k % 128, n % 16, dtype and layout enums
+    args = lambda m, n, k, dt=0, lay=0: (p16, k, p16, k, p16, k // 128 or 1, 1, p16, max(k // 128, 1), None, p16, n,
+                                         m, n, k, dt, lay, 0, None, 0, None)
+    assert L.aklr_gemm_a8w8_blockscale(*args(4, 16, 100)) == 1
+    assert L.aklr_gemm_a8w8_blockscale(*args(4, 20, 128)) == 1
+    assert L.aklr_gemm_a8w8_blockscale(*args(4, 16, 128, dt=5)) == 2
+    assert L.aklr_gemm_a8w8_blockscale(*args(4, 16, 128, lay=9)) == 2
+    assert L.aklr_gemm_a8w8_blockscale(*args(0, 16, 128)) == 0
+    a4 = lambda m, n, k: (p16, k // 2, p16, k // 2, p16, k // 32, p16, k // 32, None, p16, n, m, n, k, 0, 0, 0, None,
+                          0, None)
+    assert L.aklr_gemm_a4w4_mxfp4(*a4(4, 16, 96)) == 1
+    assert L.aklr_gemm_a4w4_mxfp4(*a4(0, 16, 64)) == 0
+
+
+def test_workspace_sizes_are_host_computable(native_lib):
+    L = native_lib
+    assert L.aklr_gemm_a8w8_blockscale_workspace_bytes(0, 16, 128) == 0
+    for m, n, k in ((1, 2112, 7168), (16, 7168, 16384), (4096, 7168, 16384), (128, 24576, 1536)):
+        ws = L.aklr_gemm_a8w8_blockscale_workspace_bytes(m, n, k)
+        assert ws % 4 == 0 and ws <= 64 * m * n * 4
+    assert L.aklr_gemm_a4w4_mxfp4_workspace_bytes(1, 10240, 8192) % 4 == 0
