@@ -22,6 +22,20 @@ __device__ __forceinline__ u32x4 ld16_nt(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// Raw buffer loads. A descriptor covers `bytes` from `base`; a load whose 32-bit offset is at or past
+// `bytes` returns zeros and touches no memory, so an offset of kOobOffset switches a load off without
+// a branch. kNt marks a stream that is read once (non-temporal).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOobOffset = 0x80000000u;
+constexpr int kNt = 2;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+template <int AUX = 0>
+__device__ __forceinline__ u32x4 buf_ld16(rsrc_t r, uint32_t voffset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voffset, 0, AUX));
+}
+
 // fl32(1/448) = 0x3B124925 (0x1.24924ap-9): the e4m3fn quantizer multiplies amax by this constant
 // (it does not divide by 448).
 constexpr float kInv448 = 0x1.24924ap-9f;
@@ -78,6 +92,46 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, float v, int o
   else
     reinterpret_cast<uint16_t*>(out)[idx] = (uint16_t)f32_to_f16_bits(v);
 }
+
+// Split-K partials: layout [split][col][m4] fp32 with m4 = m rounded up to 4, so a lane's 4 rows of
+// one column (an MFMA 16x16 accumulator's rows 4g..4g+3) are one 16-byte access and a wave's
+// accesses are contiguous runs. They travel through device-coherent (sc1) buffer accesses, which go
+// past the XCD-local caches to the memory-side coherence point without the whole-L2 write-back /
+// invalidate that an agent-scope fence costs. One descriptor per split (a split's plane is < 4 GiB).
+constexpr int kSc1 = 16;
+__device__ __forceinline__ rsrc_t partial_rsrc(float* partial, int split, int64_t plane) {
+  return make_rsrc(partial + (int64_t)split * plane, (uint32_t)(plane * 4));
+}
+__device__ __forceinline__ void store_partial4(rsrc_t r, int64_t elem, const f32x4& v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), r, (int)(elem * 4), 0, kSc1);
+}
+__device__ __forceinline__ f32x4 load_partial4(rsrc_t r, int64_t elem) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(elem * 4), 0, kSc1));
+}
+__host__ __device__ inline int64_t round4(int64_t m) { return (m + 3) / 4 * 4; }
+
+// Split-K arrival. Each workgroup of an output tile stores its fp32 partial with store_partial4,
+// then calls this (every thread of the workgroup): it waits until those stores are acknowledged,
+// bumps the tile's counter once with an agent-scope atomic, and returns true only in the workgroup
+// that arrives last. That one resets the counter to 0 for the next call and owns the reduction,
+// which it reads with load_partial4 and sums in split order, so the result does not depend on the
+// arrival order. `slot` is the workgroup's LDS word for the broadcast.
+__device__ __forceinline__ bool splitk_arrive(unsigned* counter, int splits, unsigned* slot) {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are acknowledged
+  __syncthreads();                // ... and every other wave's
+  if (threadIdx.x == 0) *slot = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const bool last = *slot == (unsigned)(splits - 1);
+  if (last && threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return last;
+}
+
+// Workspace layout of the split-K GEMMs: a fixed 64 KiB region of counters, one per output tile
+// (at most 16384: n / 16 column groups for n <= 262144, or <= 512 tiles), zero before first use
+// and left zero by every call; then fp32 partials [splits, n, round4(m)]. The region's size is the same for
+// every call, so one call's partials never land on another's counters.
+constexpr size_t kSplitkCounterBytes = 65536;
+constexpr int64_t kSplitkMaxTiles = (int64_t)(kSplitkCounterBytes / 4);
 
 }  // namespace aklr
 

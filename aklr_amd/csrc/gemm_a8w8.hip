@@ -1,18 +1,21 @@
 // 128x128-block-scaled FP8 GEMM for gfx950: out = (a * a_scale) @ (b * b_scale)^T + bias.
 //
-// Both kernels run one V_MFMA_SCALE_F32_16X16X128_F8F6F4 atom (unit e8m0 scales) per 16x16 output
-// tile per 128-wide K block, into a zero accumulator, and fold that partial into the fp32 result
+// Every kernel runs one V_MFMA_SCALE_F32_16X16X128_F8F6F4 atom (unit e8m0 scales) per 16x16 output
+// tile per 128-wide K block, into a zero accumulator, and folds that partial into the fp32 result
 // with one FMA per element: acc += partial * (a_scale[row, kb] * b_scale[n/128, kb]). The fp32 block
 // scales are not powers of two, so they cannot ride the MFMA's e8m0 scale operands.
 //
-// * decode (m <= 128): weight-streaming. A workgroup owns 16*NT output columns and a K range;
-//   each wave streams its own contiguous K sub-range of the weight straight from HBM into MFMA
-//   operand registers (no LDS), the activations come from L2. Waves are reduced through LDS in
-//   wave order; when the K range is split across workgroups too, fp32 partials go to the caller's
-//   workspace and a second kernel sums them in split order. Every sum has a fixed order, so
-//   results are bitwise reproducible.
-// * tile (m > 128): 128x128 workgroup tiles, 4 waves of 64x64, K steps of 128 double-buffered in
+// * skinny (m <= 64): weight streaming. A workgroup owns 16*NT output columns and a K range; each of
+//   its waves streams its own contiguous K sub-range of the weight straight from HBM into MFMA
+//   operand registers (no LDS), D K-blocks in flight, with the activations from L2. The waves'
+//   accumulators are summed in one LDS tile in wave order.
+// * tile (m > 64): 128x128 workgroup tiles, 4 waves of 64x64, K steps of 128 double-buffered in
 //   LDS (16-byte chunks XOR-swizzled by row), a_scale staged in LDS, XCD-aware tile order.
+//
+// When K is also split across workgroups, each stores an fp32 partial into the caller's workspace
+// and the last workgroup of the output tile to arrive (an agent-scope counter) sums the partials in
+// split order and writes the output: one launch, and every sum has a fixed order, so results are
+// bitwise reproducible.
 #include "common.h"
 
 namespace aklr {
@@ -31,7 +34,8 @@ struct Gemm8Args {
   int64_t ldo;
   int m, n, k;
   int out_dtype;
-  float* partial;  // [splits, m, n] when splits > 1
+  unsigned* counters;  // one per output tile when splits > 1
+  float* partial;      // [splits, n, round4(m)] when splits > 1
   int splits;
   int kb_per_split;
 };
@@ -45,26 +49,29 @@ __device__ __forceinline__ i32x8 cat(const u32x4& lo, const u32x4& hi) {
 
 // Offset, in a PRESHUFFLE_16x16 weight with kt32 = k/32 column tiles, of the 16 bytes that MFMA lane
 // group g (0..3) needs for row `col` and K block kb: k = 16g.. (tile 4kb + g/2, half g%2) and
-// k = 64+16g.. (tile 4kb + 2 + g/2). Returns the first; the second is +1024.
+// k = 64+16g.. (tile 4kb + 2 + g/2). Returns the first; the second is +1024. The 64 lanes of one
+// load read 1 KiB: two runs of 512 contiguous bytes.
 __device__ __forceinline__ int64_t preshuffle_frag_offset(int64_t col, int64_t kt32, int kb, int g) {
   return ((col >> 4) * kt32 + (int64_t)kb * 4 + (g >> 1)) * 512 + (g & 1) * 256 + (col & 15) * 16;
 }
 
 // ---------------------------------------------------------------------------------------------
-// decode
+// skinny
 template <int MT, int NT>
-struct DecodeFrag {
+struct SkinnyFrag {
   i32x8 a[MT];
   i32x8 b[NT];
   float sa[MT][4];
   float sb[NT];
 };
 
-template <int MT, int NT, int NW, int FMT, bool PRE>
-__global__ __launch_bounds__(NW * 64) void gemm8_decode_kernel(Gemm8Args p) {
-  static_assert(NW >= 2, "at least two waves");
-  __shared__ f32x4 red[(NW - 1) * MT * NT * 64];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+template <int MT, int NT, int NW, int D, int FMT, bool PRE>
+__global__ __launch_bounds__(NW * 64) void gemm8_skinny_kernel(Gemm8Args p) {
+  constexpr int T = MT * NT;
+  __shared__ f32x4 red[T][64];
+  __shared__ unsigned arrive_slot;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: K ranges live in SGPRs
   const int li = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16 * NT;
   const int split = blockIdx.y;
@@ -76,62 +83,58 @@ __global__ __launch_bounds__(NW * 64) void gemm8_decode_kernel(Gemm8Args p) {
   const int kb_end = kb_base + min((w + 1) * chunk, kb_len);
   const int64_t kt32 = p.k >> 5;
 
-  const uint8_t* bp[NT];
-  bool bval[NT];
+  // A and B come through raw buffer loads whose per-block offset is switched off (kOobOffset: zeros,
+  // no memory access) past the wave's K range, so the loop below refills its register ring with no
+  // branch. Rows past m and column tiles past n read row/tile 0 instead: they only feed output rows
+  // and columns that are never stored. B gets one descriptor per 16-column tile (offsets < 16*ldb).
+  rsrc_t brs[NT];
   const float* sbp[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int64_t col = n0 + nt * 16 + li;
-    bval[nt] = (n0 + nt * 16) < p.n;  // n % 16 == 0: validity is uniform per 16-column tile
+    const int64_t c0 = (n0 + nt * 16) < p.n ? n0 + nt * 16 : 0;  // n % 16 == 0: validity per tile
     if (PRE)
-      bp[nt] = p.b + preshuffle_frag_offset(bval[nt] ? col : 0, kt32, 0, g);
+      brs[nt] = make_rsrc(p.b + (c0 >> 4) * kt32 * 512, (uint32_t)(kt32 * 512));
     else
-      bp[nt] = p.b + (bval[nt] ? col : 0) * p.ldb + g * 16;
-    sbp[nt] = p.sb + (int64_t)((bval[nt] ? n0 + nt * 16 : 0) >> 7) * p.ldbs;
+      brs[nt] = make_rsrc(p.b + c0 * p.ldb, (uint32_t)(15 * p.ldb + p.k));
+    sbp[nt] = p.sb + (c0 >> 7) * p.ldbs;
   }
-  const uint8_t* ap[MT];
-  bool aval[MT];
-  const float* sap[MT][4];
-  bool sval[MT][4];
+  const uint32_t b_lane = PRE ? (uint32_t)((g >> 1) * 512 + (g & 1) * 256 + li * 16)
+                              : (uint32_t)(li * p.ldb + g * 16);
+  // Activation fragments and a_scale are loaded only by lanes whose rows exist: the others get the
+  // out-of-range offset (zeros, no request), which for m < 16 removes most of their L2 traffic.
+  const rsrc_t ars = make_rsrc(p.a, (uint32_t)((p.m - 1) * p.lda + p.k));
+  const rsrc_t sars = make_rsrc(p.sa, (uint32_t)(((p.m - 1) * p.sa_sm + (KB - 1) * p.sa_sk + 1) * 4));
+  uint32_t a_lane[MT];
+  uint32_t sa_lane[MT][4];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int row = mt * 16 + li;
-    aval[mt] = row < p.m;
-    ap[mt] = p.a + (int64_t)(aval[mt] ? row : 0) * p.lda + g * 16;
+    a_lane[mt] = row < p.m ? (uint32_t)(row * p.lda + g * 16) : kOobOffset;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int srow = mt * 16 + 4 * g + r;
-      sval[mt][r] = srow < p.m;
-      sap[mt][r] = p.sa + (int64_t)(sval[mt][r] ? srow : 0) * p.sa_sm;
+      sa_lane[mt][r] = srow < p.m ? (uint32_t)(srow * p.sa_sm * 4) : kOobOffset;
     }
   }
+  const uint32_t sa_kstep = (uint32_t)(p.sa_sk * 4);
 
-  auto load = [&](int kb, DecodeFrag<MT, NT>& f) {
+  auto load = [&](int kb, SkinnyFrag<MT, NT>& f) {
+    const bool on = kb < kb_end;
+    const int kbc = min(kb, KB - 1);  // b_scale: any valid block (its product with zero data is 0)
+    const uint32_t boff = on ? (uint32_t)(PRE ? kb * 2048 : kb * 128) : kOobOffset;
+    const uint32_t aoff = on ? (uint32_t)(kb * 128) : kOobOffset;
+    const uint32_t soff = on ? (uint32_t)kb * sa_kstep : kOobOffset;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      u32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
-      if (bval[nt]) {
-        if (PRE) {
-          lo = ld16_nt(bp[nt] + (int64_t)kb * 2048);
-          hi = ld16_nt(bp[nt] + (int64_t)kb * 2048 + 1024);
-        } else {
-          lo = ld16_nt(bp[nt] + (int64_t)kb * 128);
-          hi = ld16_nt(bp[nt] + (int64_t)kb * 128 + 64);
-        }
-      }
-      f.b[nt] = cat(lo, hi);
-      f.sb[nt] = bval[nt] ? sbp[nt][kb] : 0.0f;
+      f.b[nt] = cat(buf_ld16<kNt>(brs[nt], b_lane + boff), buf_ld16<kNt>(brs[nt], b_lane + boff + (PRE ? 1024 : 64)));
+      f.sb[nt] = sbp[nt][kbc];
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      u32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
-      if (aval[mt]) {
-        lo = ld16(ap[mt] + (int64_t)kb * 128);
-        hi = ld16(ap[mt] + (int64_t)kb * 128 + 64);
-      }
-      f.a[mt] = cat(lo, hi);
+      f.a[mt] = cat(buf_ld16(ars, a_lane[mt] + aoff), buf_ld16(ars, a_lane[mt] + aoff + 64));
 #pragma unroll
-      for (int r = 0; r < 4; ++r) f.sa[mt][r] = sval[mt][r] ? sap[mt][r][(int64_t)kb * p.sa_sk] : 0.0f;
+      for (int r = 0; r < 4; ++r)
+        f.sa[mt][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sars, (int)(sa_lane[mt][r] + soff), 0, 0));
     }
   };
 
@@ -141,89 +144,81 @@ __global__ __launch_bounds__(NW * 64) void gemm8_decode_kernel(Gemm8Args p) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  if (kb_begin < kb_end) {
-    DecodeFrag<MT, NT> cur, nxt;
-    load(kb_begin, cur);
-    for (int kb = kb_begin; kb < kb_end; ++kb) {
-      if (kb + 1 < kb_end) load(kb + 1, nxt);
+  // D-deep register ring: block kb0 + j lives in f[j]; once consumed, the slot is refilled with block
+  // kb0 + j + D. Blocks past kb_end load as zeros, so the last group needs no special case.
+  SkinnyFrag<MT, NT> f[D];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
+  for (int j = 0; j < D; ++j) load(kb_begin + j, f[j]);
+  for (int kb0 = kb_begin; kb0 < kb_end; kb0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-          const f32x4 part = mfma16x128<FMT>(cur.a[mt], cur.b[nt], z);
+          const f32x4 part = mfma16x128<FMT>(f[j].a[mt], f[j].b[nt], z);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(part[r], cur.sa[mt][r] * cur.sb[nt], acc[mt][nt][r]);
+          for (int r = 0; r < 4; ++r)
+            acc[mt][nt][r] = fmaf(part[r], f[j].sa[mt][r] * f[j].sb[nt], acc[mt][nt][r]);
         }
-      }
-      cur = nxt;
+      load(kb0 + j + D, f[j]);
+      __builtin_amdgcn_sched_barrier(0);  // refill slot j before consuming slot j + 1
     }
   }
 
-  // Fixed-order reduction over the waves: wave 0 adds waves 1, 2, ... in turn.
-  if (w > 0) {
+  // Sum the waves' accumulators in wave order: wave 0 stores, waves 1.. NW-1 add in turn.
+  for (int v = 0; v < NW; ++v) {
+    if (w == v) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) red[(((w - 1) * MT + mt) * NT + nt) * 64 + lane] = acc[mt][nt];
-  }
-  __syncthreads();
-  if (w != 0) return;
-#pragma unroll
-  for (int v = 1; v < NW; ++v)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const f32x4 o = red[(((v - 1) * MT + mt) * NT + nt) * 64 + lane];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mt][nt][r] += o[r];
-      }
-
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      if (!bval[nt]) continue;
-      const int col = n0 + nt * 16 + li;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = mt * 16 + 4 * g + r;
-        if (row >= p.m) continue;
-        if (p.splits > 1) {
-          p.partial[((int64_t)split * p.m + row) * p.n + col] = acc[mt][nt][r];
-        } else {
-          float v = acc[mt][nt][r];
-          if (p.bias) v += p.bias[col];
-          store_out(p.out, (int64_t)row * p.ldo + col, v, p.out_dtype);
+        for (int nt = 0; nt < NT; ++nt) {
+          const int t = mt * NT + nt;
+          red[t][lane] = v == 0 ? acc[mt][nt] : red[t][lane] + acc[mt][nt];
         }
-      }
     }
-}
-
-// out[row, col] = sum over splits, in split order, of partial[s, row, col] (+ bias[col]).
-__global__ __launch_bounds__(256) void gemm8_splitk_reduce_kernel(const float* __restrict__ partial, int splits,
-                                                                  int m, int n, const float* __restrict__ bias,
-                                                                  void* out, int64_t ldo, int out_dtype) {
-  const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-  const int64_t total = (int64_t)m * n;
-  if (idx >= total) return;
-  const int row = (int)(idx / n), col = (int)(idx % n);  // n % 4 == 0: the 4 columns share a row
-  f32x4 s = *reinterpret_cast<const f32x4*>(partial + idx);
-  for (int sp = 1; sp < splits; ++sp) {
-    const f32x4 o = *reinterpret_cast<const f32x4*>(partial + (int64_t)sp * total + idx);
-    s += o;
+    __syncthreads();
   }
+
+  // Wave w owns tiles t = w, w + NW, ...: it writes the output (one split) or its fp32 partial.
+  const int64_t m4 = round4(p.m);
+  const int64_t plane = (int64_t)p.n * m4;
+  for (int t = w; t < T; t += NW) {
+    const int mt = t / NT, nt = t % NT;
+    const int c0 = n0 + nt * 16;
+    if (c0 >= p.n) continue;
+    const f32x4 s = red[t][lane];
+    const int col = c0 + li;
+    const int row0 = mt * 16 + 4 * g;
+    if (p.splits > 1) {
+      if (row0 < p.m) store_partial4(partial_rsrc(p.partial, split, plane), (int64_t)col * m4 + row0, s);
+      continue;
+    }
+    const float bv = p.bias ? p.bias[col] : 0.0f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float v = s[j];
-    if (bias) v += bias[col + j];
-    store_out(out, (int64_t)row * ldo + col + j, v, out_dtype);
+    for (int r = 0; r < 4; ++r)
+      if (row0 + r < p.m) store_out(p.out, (int64_t)(row0 + r) * p.ldo + col, s[r] + bv, p.out_dtype);
+  }
+  if (p.splits == 1) return;
+  if (!splitk_arrive(p.counters + blockIdx.x, p.splits, &arrive_slot)) return;
+  for (int t = w; t < T; t += NW) {
+    const int mt = t / NT, nt = t % NT;
+    const int c0 = n0 + nt * 16;
+    const int row0 = mt * 16 + 4 * g;
+    if (c0 >= p.n || row0 >= p.m) continue;
+    const int col = c0 + li;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < p.splits; ++sp) v += load_partial4(partial_rsrc(p.partial, sp, plane), (int64_t)col * m4 + row0);
+    const float bv = p.bias ? p.bias[col] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (row0 + r < p.m) store_out(p.out, (int64_t)(row0 + r) * p.ldo + col, v[r] + bv, p.out_dtype);
   }
 }
 
 // ---------------------------------------------------------------------------------------------
-// tile (prefill)
+// tile
 constexpr int kTileM = 128, kTileN = 128;
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
@@ -233,6 +228,7 @@ __global__ __launch_bounds__(256) void gemm8_tile_kernel(Gemm8Args p) {
   __shared__ __attribute__((aligned(16))) uint8_t sA[2][kTileM * 128];
   __shared__ __attribute__((aligned(16))) uint8_t sB[2][kTileN * 128];
   __shared__ __attribute__((aligned(16))) float sSA[2][kTileM];
+  __shared__ unsigned arrive_slot;
 
   const int tiles_m = (p.m + kTileM - 1) / kTileM;
   const int tiles_n = (p.n + kTileN - 1) / kTileN;
@@ -351,20 +347,42 @@ __global__ __launch_bounds__(256) void gemm8_tile_kernel(Gemm8Args p) {
     __syncthreads();
   }
 
+  if (p.splits > 1) {
+    const int64_t m4 = round4(p.m);
+    const int64_t plane = (int64_t)p.n * m4;
+    const rsrc_t prs = partial_rsrc(p.partial, split, plane);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int col = n0 + wn * 64 + nt * 16 + li;
+        const int row0 = m0 + wm * 64 + mt * 16 + 4 * g;
+        if (col < p.n && row0 < p.m) store_partial4(prs, (int64_t)col * m4 + row0, acc[mt][nt]);
+      }
+    if (!splitk_arrive(p.counters + pid, p.splits, &arrive_slot)) return;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int col = n0 + wn * 64 + nt * 16 + li;
+        const int row0 = m0 + wm * 64 + mt * 16 + 4 * g;
+        if (col >= p.n || row0 >= p.m) continue;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        for (int sp = 0; sp < p.splits; ++sp) v += load_partial4(partial_rsrc(p.partial, sp, plane), (int64_t)col * m4 + row0);
+        const float bv = p.bias ? p.bias[col] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (row0 + r < p.m) store_out(p.out, (int64_t)(row0 + r) * p.ldo + col, v[r] + bv, p.out_dtype);
+      }
+    return;
+  }
+
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
       const int col = n0 + wn * 64 + nt * 16 + li;
       if (col >= p.n) continue;
-      if (p.splits > 1) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = m0 + wm * 64 + mt * 16 + 4 * g + r;
-          if (row < p.m) p.partial[((int64_t)split * p.m + row) * p.n + col] = acc[mt][nt][r];
-        }
-        continue;
-      }
       const float bv = p.bias ? p.bias[col] : 0.0f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -377,101 +395,97 @@ __global__ __launch_bounds__(256) void gemm8_tile_kernel(Gemm8Args p) {
 // ---------------------------------------------------------------------------------------------
 // host-side planning
 
-// m <= kDecodeMaxM streams the weight through the decode kernel; larger m runs the MFMA tile kernel.
-static constexpr int64_t kDecodeMaxM = 32;
+// m <= kSkinnyMaxM streams the weight through the skinny kernel; larger m runs the MFMA tile kernel.
+static constexpr int64_t kSkinnyMaxM = 64;
 
-struct DecodePlan {
-  int mt, nw, splits, kb_per_split;
+struct Plan8 {
+  bool skinny;
+  int mt, nt, nw;    // skinny: 16-row and 16-column tiles per wave, waves per workgroup
+  int grid_x;        // skinny: column groups; tile: output tiles
+  int splits, kb_per_split;
 };
 
-static DecodePlan plan_decode(int64_t m, int64_t n, int64_t k) {
-  DecodePlan d;
-  d.mt = m <= 16 ? 1 : 2;
-  const int KB = (int)(k / 128);
-  const int64_t n_tiles = (n + 15) / 16;
-  // Waves per workgroup: double until ~2048 waves cover the weight (8 per CU), each wave keeping
-  // at least 2 K blocks.
-  d.nw = 4;
-  while (d.nw < 16 && n_tiles * d.nw < 2048 && KB >= 4 * d.nw) d.nw *= 2;
-  // Split K across workgroups only when the columns alone give too few waves, keeping at least
-  // 2 K blocks per wave and the fp32 partial traffic (8 bytes per output per split) under ~15% of
-  // the weight bytes.
+// Skinny plan (measured on MI355X over the DeepSeek-V3 decode shapes, weights streamed from HBM):
+// one 16-column tile per wave while the activations are a few rows (two once n >= 16384, which
+// leaves >= 512 groups), two at m <= 16, four at m <= 32, and at m <= 64 four when K is long (>= 64
+// blocks) else two, so activation re-reads from L2 stay a fraction of the weight bytes; waves per
+// workgroup sized for ~2048 streaming waves chip-wide (4 or 8, each wave >= 2 K blocks); K split
+// across two workgroups only when that still leaves fewer than 1024 waves, since the split's
+// coherent hand-off costs about a kernel launch. Row tiles 1-2 keep two K blocks in flight per
+// wave; four row tiles keep one (their registers would otherwise spill).
+static Plan8 plan8(int64_t m, int64_t n, int64_t k) {
+  Plan8 p;
+  const int64_t KB = k / 128;
   int64_t s = 1;
-  if (n_tiles * d.nw < 1024) {
-    s = (2048 + n_tiles * d.nw - 1) / (n_tiles * d.nw);
-    int64_t s_max = KB / (2 * d.nw);
-    const int64_t s_traffic = (int64_t)(0.15 * (double)k / (8.0 * (double)m));
-    if (s_traffic < s_max) s_max = s_traffic;
-    if (s > s_max) s = s_max;
-    if (s < 1) s = 1;
+  if (m <= kSkinnyMaxM) {
+    p.skinny = true;
+    p.mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+    if (p.mt == 4)
+      p.nt = KB >= 64 ? 4 : 2;
+    else
+      p.nt = m <= 8 ? (n >= 16384 ? 2 : 1) : (m <= 16 ? 2 : 4);
+    const int64_t groups = (n + 16 * p.nt - 1) / (16 * p.nt);
+    p.grid_x = (int)groups;
+    p.nw = (2048 / groups >= 8 && KB >= 16 && !(p.mt == 4 && p.nt == 4)) ? 8 : 4;
+    if (groups * p.nw < 1024 && KB >= 4 * p.nw) s = 2;
+  } else {
+    p.skinny = false;
+    p.mt = p.nt = p.nw = 0;
+    const int64_t tiles = ((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN);
+    p.grid_x = (int)tiles;
+    // Split K when the tiles alone leave CUs idle: aim at 2 workgroups per CU (512), keep at least 4
+    // K blocks per split, and keep the fp32 partials within the weight's own bytes.
+    if (tiles < 512) {
+      s = (512 + tiles - 1) / tiles;
+      int64_t s_max = KB / 4;
+      const int64_t s_traffic = k / (8 * m);
+      if (s_traffic < s_max) s_max = s_traffic;
+      if (s > s_max) s = s_max;
+    }
   }
-  d.kb_per_split = (int)((KB + s - 1) / s);
-  d.splits = (int)((KB + d.kb_per_split - 1) / d.kb_per_split);
-  return d;
+  if (s < 1 || p.grid_x > kSplitkMaxTiles) s = 1;  // one counter per output tile must fit the region
+  p.kb_per_split = (int)((KB + s - 1) / s);
+  p.splits = (int)((KB + p.kb_per_split - 1) / p.kb_per_split);
+  return p;
 }
 
-struct TilePlan {
-  int tiles, splits, kb_per_split;
-};
-
-static TilePlan plan_tile(int64_t m, int64_t n, int64_t k) {
-  TilePlan t;
-  t.tiles = (int)(((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN));
-  const int KB = (int)(k / 128);
-  // Split K when the tiles alone leave CUs idle: aim at 2 workgroups per CU (512), keep at least 4
-  // K blocks per split, and keep the fp32 partials (8 bytes per output per split, written then
-  // summed) within the weight's own bytes.
-  int64_t s = 1;
-  if (t.tiles < 512) {
-    s = (512 + t.tiles - 1) / t.tiles;
-    int64_t s_max = KB / 4;
-    const int64_t s_traffic = k / (8 * m);
-    if (s_traffic < s_max) s_max = s_traffic;
-    if (s > s_max) s = s_max;
-    if (s < 1) s = 1;
-  }
-  t.kb_per_split = (int)((KB + s - 1) / s);
-  t.splits = (int)((KB + t.kb_per_split - 1) / t.kb_per_split);
-  return t;
+static size_t workspace8(const Plan8& p, int64_t m, int64_t n) {
+  if (p.splits <= 1) return 0;
+  return kSplitkCounterBytes + (size_t)p.splits * (size_t)round4(m) * (size_t)n * sizeof(float);
 }
 
-template <int MT, int NW, int FMT, bool PRE>
-static void launch_decode(const Gemm8Args& a, const DecodePlan& d, hipStream_t s) {
-  dim3 grid((unsigned)((a.n + 15) / 16), (unsigned)d.splits);
-  hipLaunchKernelGGL((gemm8_decode_kernel<MT, 1, NW, FMT, PRE>), grid, dim3(NW * 64), 0, s, a);
+template <int MT, int NT, int NW, int FMT, bool PRE>
+static void launch_skinny(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
+  constexpr int D = MT >= 4 ? 1 : 2;
+  dim3 grid((unsigned)d.grid_x, (unsigned)d.splits);
+  hipLaunchKernelGGL((gemm8_skinny_kernel<MT, NT, NW, D, FMT, PRE>), grid, dim3(NW * 64), 0, s, a);
+}
+
+template <int MT, int NT, int FMT, bool PRE>
+static void dispatch_skinny_nw(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
+  if (d.nw == 8) launch_skinny<MT, NT, 8, FMT, PRE>(a, d, s);
+  else launch_skinny<MT, NT, 4, FMT, PRE>(a, d, s);
+}
+
+template <int MT, int FMT, bool PRE>
+static void dispatch_skinny_nt(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
+  if (d.nt == 4) dispatch_skinny_nw<MT, 4, FMT, PRE>(a, d, s);
+  else if (d.nt == 2) dispatch_skinny_nw<MT, 2, FMT, PRE>(a, d, s);
+  else dispatch_skinny_nw<MT, 1, FMT, PRE>(a, d, s);
 }
 
 template <int FMT, bool PRE>
-static void dispatch_decode(const Gemm8Args& a, const DecodePlan& d, hipStream_t s) {
-  if (d.mt == 1) {
-    if (d.nw == 16) launch_decode<1, 16, FMT, PRE>(a, d, s);
-    else if (d.nw == 8) launch_decode<1, 8, FMT, PRE>(a, d, s);
-    else launch_decode<1, 4, FMT, PRE>(a, d, s);
-  } else {
-    if (d.nw == 16) launch_decode<2, 16, FMT, PRE>(a, d, s);
-    else if (d.nw == 8) launch_decode<2, 8, FMT, PRE>(a, d, s);
-    else launch_decode<2, 4, FMT, PRE>(a, d, s);
-  }
+static void dispatch_skinny(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
+  if (d.mt == 1) dispatch_skinny_nt<1, FMT, PRE>(a, d, s);
+  else if (d.mt == 2) dispatch_skinny_nt<2, FMT, PRE>(a, d, s);
+  else if (d.nt == 4) launch_skinny<4, 4, 4, FMT, PRE>(a, d, s);  // 4x4 tiles run with 4 waves only
+  else if (d.nw == 8) launch_skinny<4, 2, 8, FMT, PRE>(a, d, s);
+  else launch_skinny<4, 2, 4, FMT, PRE>(a, d, s);
 }
 
 template <int FMT, bool PRE>
-static void launch_tile(const Gemm8Args& a, const TilePlan& t, hipStream_t s) {
-  hipLaunchKernelGGL((gemm8_tile_kernel<FMT, PRE>), dim3((unsigned)(t.tiles * t.splits)), dim3(256), 0, s, a);
-}
-
-// Splits and K blocks per split of the kernel that will serve (m, n, k); returns the workspace
-// bytes it needs (fp32 partials [splits, m, n] when splits > 1).
-static size_t plan_splits(int64_t m, int64_t n, int64_t k, int* splits, int* kb_per_split) {
-  if (m <= kDecodeMaxM) {
-    const DecodePlan d = plan_decode(m, n, k);
-    *splits = d.splits;
-    *kb_per_split = d.kb_per_split;
-  } else {
-    const TilePlan t = plan_tile(m, n, k);
-    *splits = t.splits;
-    *kb_per_split = t.kb_per_split;
-  }
-  return *splits > 1 ? (size_t)*splits * (size_t)m * (size_t)n * sizeof(float) : 0;
+static void launch_tile(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
+  hipLaunchKernelGGL((gemm8_tile_kernel<FMT, PRE>), dim3((unsigned)(t.grid_x * t.splits)), dim3(256), 0, s, a);
 }
 
 }  // namespace aklr
@@ -480,8 +494,7 @@ using namespace aklr;
 
 extern "C" size_t aklr_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k < 128) return 0;
-  int splits, kps;
-  return plan_splits(m, n, k, &splits, &kps);
+  return workspace8(plan8(m, n, k), m, n);
 }
 
 extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void* b, int64_t ldb,
@@ -522,33 +535,27 @@ extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void*
   g.n = (int)n;
   g.k = (int)k;
   g.out_dtype = out_dtype;
+  g.counters = nullptr;
   g.partial = nullptr;
   const bool pre = b_layout == AKLR_B_PRESHUFFLE_16x16;
   const bool e5 = fp8_dtype == AKLR_FP8_E5M2;
 
-  int splits, kps;
-  const size_t need = plan_splits(m, n, k, &splits, &kps);
-  g.splits = splits;
-  g.kb_per_split = kps;
-  if (splits > 1) {
+  const Plan8 plan = plan8(m, n, k);
+  g.splits = plan.splits;
+  g.kb_per_split = plan.kb_per_split;
+  if (plan.splits > 1) {
+    const size_t need = workspace8(plan, m, n);
     if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) return AKLR_ERR_WORKSPACE;
-    g.partial = static_cast<float*>(workspace);
+    g.counters = static_cast<unsigned*>(workspace);
+    g.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kSplitkCounterBytes);
   }
-  if (m <= kDecodeMaxM) {
-    const DecodePlan d = plan_decode(m, n, k);
-    if (e5) pre ? dispatch_decode<1, true>(g, d, stream) : dispatch_decode<1, false>(g, d, stream);
-    else pre ? dispatch_decode<0, true>(g, d, stream) : dispatch_decode<0, false>(g, d, stream);
+  if (plan.skinny) {
+    if (e5) pre ? dispatch_skinny<1, true>(g, plan, stream) : dispatch_skinny<1, false>(g, plan, stream);
+    else pre ? dispatch_skinny<0, true>(g, plan, stream) : dispatch_skinny<0, false>(g, plan, stream);
   } else {
-    const TilePlan t = plan_tile(m, n, k);
-    if (e5) pre ? launch_tile<1, true>(g, t, stream) : launch_tile<1, false>(g, t, stream);
-    else pre ? launch_tile<0, true>(g, t, stream) : launch_tile<0, false>(g, t, stream);
+    if (e5) pre ? launch_tile<1, true>(g, plan, stream) : launch_tile<1, false>(g, plan, stream);
+    else pre ? launch_tile<0, true>(g, plan, stream) : launch_tile<0, false>(g, plan, stream);
   }
   AKLR_LAUNCH_CHECK();
-  if (splits > 1) {
-    const int64_t quads = (m * n) / 4;
-    hipLaunchKernelGGL(gemm8_splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
-                       g.partial, splits, g.m, g.n, bias, out, ldo, out_dtype);
-    AKLR_LAUNCH_CHECK();
-  }
   return AKLR_OK;
 }

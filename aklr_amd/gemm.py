@@ -25,7 +25,7 @@ from dataclasses import dataclass, field
 
 import torch
 
-from . import _lib
+from . import _lib, workspace
 from .dispatch import FallbackReason, aligned, api, on_gpu, overlaps
 
 _FP8 = {torch.float8_e4m3fn: _lib.FP8_E4M3FN, torch.float8_e5m2: _lib.FP8_E5M2}
@@ -86,7 +86,7 @@ def _run_gemm8(p: _Gemm8Plan):
     out = p.out if p.out is not None else torch.empty((p.m, p.n), dtype=p.out_dtype, device=dev)
     L = _lib.lib()
     ws_bytes = L.aklr_gemm_a8w8_blockscale_workspace_bytes(p.m, p.n, p.k)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    ws = workspace.get(dev, ws_bytes)
     st = L.aklr_gemm_a8w8_blockscale(
         p.a.data_ptr(), p.a.stride(0), p.b.data_ptr(), p.b.stride(0) if p.b_layout == _lib.B_ROW_MAJOR else p.k,
         p.a_scale.data_ptr(), p.sa_sm, p.sa_sk, p.b_scale.data_ptr(), p.b_scale.stride(0),
@@ -182,8 +182,10 @@ def gemm_a8w8_blockwise_scaled(
         return _OOC
     if not trans_b:
         return FallbackReason.NO_WORKLOAD
+    if not workspace.ready(a.device, _lib.lib().aklr_gemm_a8w8_blockscale_workspace_bytes(m, n, k)):
+        return FallbackReason.NOT_WARMED
     b_layout = _lib.B_ROW_MAJOR if variant == "row_major" else _lib.B_PRESHUFFLE_16x16
-    path = "decode" if m <= 32 else "tile"  # the library picks the same way (kDecodeMaxM)
+    path = "skinny" if m <= 64 else "tile"  # the library picks the same way (kSkinnyMaxM)
     return _Gemm8Plan(a, b, a_scale, b_scale, bias, out, dt, m, n, k, sa_sm, sa_sk, b_layout, variant,
                       f"aklr_gemm_a8w8_blockscale:{path}")
 
@@ -216,7 +218,7 @@ def _run_gemm4(p: _Gemm4Plan):
     out = p.out if p.out is not None else torch.empty((p.m, p.n), dtype=p.out_dtype, device=dev)
     L = _lib.lib()
     ws_bytes = L.aklr_gemm_a4w4_mxfp4_workspace_bytes(p.m, p.n, p.k)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    ws = workspace.get(dev, ws_bytes)
     a, b, sa, sb = _u8(p.a), _u8(p.b), _u8(p.a_scale), _u8(p.b_scale)
     st = L.aklr_gemm_a4w4_mxfp4(
         a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), sa.data_ptr(), sa.stride(0), sb.data_ptr(),
@@ -291,6 +293,8 @@ def gemm_a4w4_mxfp4(
         return _OOC
     if not _out_ok(out, m, n, dt, a.device, (a, b, a_scale, b_scale, bias)):
         return _OOC
+    if not workspace.ready(a.device, _lib.lib().aklr_gemm_a4w4_mxfp4_workspace_bytes(m, n, k)):
+        return FallbackReason.NOT_WARMED
     pre = variant == "b_shuffled"
     path = "decode" if m <= 32 else "tile"
     return _Gemm4Plan(a, b, a_scale, b_scale, bias, out, dt, m, n, k,

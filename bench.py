@@ -10,8 +10,8 @@ Each step is one HIP graph; steps rotate over enough weight copies (> 512 MB per
 
 value = whole-step algorithmic bytes / step time, in GB/s (bytes per GEMM: M*K + 4*M*K/128 + N*K +
 4*ceil(N/128)*K/128 + 2*M*N; per quant: 3.03125*M*K).
-roofline: the dominant kernel, the decode GEMM at M=16, (N, K) = (7168, 16384) (117.97 MB per launch),
-timed alone with HIP events on its stream over graph replays; peak 8 TB/s.
+roofline: the dominant kernel, the skinny (decode) GEMM at M=16, (N, K) = (7168, 16384) (117.97 MB per
+launch), timed alone with HIP events on its stream over graph replays; peak 8 TB/s.
 prefill / mxfp4: extra figures (TFLOP/s vs the dense FP8 5.0 PF / MXFP4 10.1 PF peaks) at M=4096.
 cpu_baseline: the CPU oracle (numpy dequantize + fp32 matmul, the reference check's formula) on a
 bounded sample (decode M=16, the three shapes), timed on the host in the same run.
@@ -256,7 +256,7 @@ def main(argv=None):
     achieved = dom_bytes / (t_dom * 1e-3) / 1e9
     per_shape = []
     for (n, k) in ((2112, 7168), (24576, 1536), (7168, 16384)):
-        for m in (1, 16, 128):
+        for m in (1, 16, 64, 128):
             t = time_gemm8(dev, m, n, k, weights, 10, stream, shuffled)
             per_shape.append({"m": m, "n": n, "k": k, "us": round(t * 1e3, 2),
                               "gbs": round(gemm8_bytes(m, n, k) / (t * 1e-3) / 1e9, 1)})
@@ -297,7 +297,7 @@ def main(argv=None):
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"gemm8_decode_kernel (M={m_dom}, N={n_dom}, K={k_dom})",
+            "kernel": f"gemm8_skinny_kernel (M={m_dom}, N={n_dom}, K={k_dom})",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -6,9 +6,11 @@
  * the current device. It returns AKLR_OK or a nonzero status (aklr_status_string names it).
  * Entry points are stateless and may be called from any host thread with its own stream.
  *
- * Scratch memory (split-K partials) is brought by the caller: ask *_workspace_bytes() for the
- * size, pass a device buffer at least that large (16-byte aligned). The library keeps nothing
- * between calls.
+ * Scratch memory is brought by the caller: ask *_workspace_bytes() for the size and pass a device
+ * buffer at least that large (16-byte aligned). Its first 64 KiB are split-K arrival counters: they
+ * must be zero before the buffer's first use, and every call leaves them zero again, so one buffer
+ * serves any sequence of calls on one stream (calls that may run concurrently need their own
+ * buffers). The rest holds fp32 partials. The library keeps nothing between calls.
  *
  * Each entry point replaces one kernel ABI of the reference (a TORCH_LIBRARY `run(...)` op that
  * AKLR's HipBuilder loads); the citation is on each declaration.

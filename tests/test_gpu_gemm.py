@@ -210,3 +210,12 @@ def test_quant_gemm_pipeline_matches_oracle_end_to_end():
     q_ref, s_ref = oquant.per_group_quant_fp8(bf16_bits(x))
     ref = ogemm.gemm_a8w8_blockwise_scaled(q_ref, u8(b), s_ref, bs.cpu().numpy(), scale_major_mode="MN")
     _check(out, ref, "pipeline")
+
+
+def test_workspace_shared_across_shapes():
+    # one stream's split-K workspace serves calls of different plans in any order: a call with few
+    # column groups and many splits, then one with many column groups, then the first again
+    shapes = [(1, 2112, 7168), (1, 24576, 1536), (16, 7168, 16384), (1, 2112, 7168), (128, 2112, 7168),
+              (1, 24576, 1536)]
+    for i, (m, n, k) in enumerate(shapes):
+        _run_and_check(m, n, k, variant="b_shuffled", rows=128, cols=2048, seed=60 + i)
