@@ -36,6 +36,44 @@ __device__ __forceinline__ u32x4 buf_ld16(rsrc_t r, uint32_t voffset) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voffset, 0, AUX));
 }
 
+// Direct-to-LDS buffer loads: lane i of the wave writes its 16 (or 4) bytes at lds + i * 16 (i * 4), so
+// the LDS placement is fixed by the lane and the global address each lane picks sets the layout.
+// An out-of-range offset (kOobOffset) reads zeros.
+typedef __attribute__((address_space(3))) void lds_void;
+// The same 16-byte direct-to-LDS load issued from inline assembly, with a descriptor built by
+// make_rsrc_words. The compiler's wait-count pass does not see it, so it adds no conservative wait
+// before later LDS reads of other buffers; the caller waits (s_waitcnt vmcnt) and synchronises
+// itself before reading what it loaded. `lds` must be wave-uniform. The statement declares no memory
+// clobber, so loads of read-only kernel inputs after it can still go through the scalar unit;
+// callers order it against LDS reads with barriers.
+__device__ __forceinline__ i32x4 make_rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)((uint32_t)(a >> 32) & 0xFFFFu);
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;
+  return r;
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void lds_dma16(const i32x4& rsrc, uint32_t lds, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voffset), "s"(rsrc)
+               : "m0");
+}
+__device__ __forceinline__ void lds_dma4(const i32x4& rsrc, uint32_t lds, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(lds), "v"(voffset), "s"(rsrc)
+               : "m0");
+}
+
+__device__ __forceinline__ void buf_ld_lds16(rsrc_t r, void* lds, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, (int)voffset, 0, 0, 0);
+}
+__device__ __forceinline__ void buf_ld_lds4(rsrc_t r, void* lds, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 4, (int)voffset, 0, 0, 0);
+}
+
 // fl32(1/448) = 0x3B124925 (0x1.24924ap-9): the e4m3fn quantizer multiplies amax by this constant
 // (it does not divide by 448).
 constexpr float kInv448 = 0x1.24924ap-9f;

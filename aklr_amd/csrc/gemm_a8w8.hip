@@ -9,8 +9,9 @@
 //   its waves streams its own contiguous K sub-range of the weight straight from HBM into MFMA
 //   operand registers (no LDS), D K-blocks in flight, with the activations from L2. The waves'
 //   accumulators are summed in one LDS tile in wave order.
-// * tile (m > 64): 128x128 workgroup tiles, 4 waves of 64x64, K steps of 128 double-buffered in
-//   LDS (16-byte chunks XOR-swizzled by row), a_scale staged in LDS, XCD-aware tile order.
+// * lds (m > 64): 256x256, 256x128, 128x256 or 128x128 workgroup tiles of 8 waves, K steps of 128
+//   through a 2- to 4-stage LDS ring filled by direct-to-LDS loads (16-byte chunks XOR-swizzled by
+//   row), a_scale staged in LDS, XCD-aware tile order, 16-byte output stores.
 //
 // When K is also split across workgroups, each stores an fp32 partial into the caller's workspace
 // and the last workgroup of the output tile to arrive (an agent-scope counter) sums the partials in
@@ -35,7 +36,7 @@ struct Gemm8Args {
   int m, n, k;
   int out_dtype;
   unsigned* counters;  // one per output tile when splits > 1
-  float* partial;      // [splits, n, round4(m)] when splits > 1
+  float* partial;      // when splits > 1: skinny [splits, n, round4(m)], lds [splits, m, n]
   int splits;
   int kb_per_split;
 };
@@ -218,192 +219,315 @@ __global__ __launch_bounds__(NW * 64) void gemm8_skinny_kernel(Gemm8Args p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// tile
-constexpr int kTileM = 128, kTileN = 128;
+// lds (m > 64): TM x TN workgroup tiles, 8 waves in 2 (m) x 4 (n), each wave (TM/2) x (TN/4), K steps
+// of 128 through an S-stage LDS ring that S - 1 stages fill ahead of the compute. A, B and a_scale go
+// global -> LDS with direct-to-LDS buffer loads (no register staging), every wave issuing the same
+// number of loads per stage, so one immediate wait count leaves exactly S - 2 stages in flight.
+// Each LDS operand tile is rows of 128 bytes with the 16-byte chunks XOR-swizzled by row (chunk c of
+// row r at position c ^ (r & 7)): lane i of a load writes position i % 8 of row i / 8 of its 8-row
+// slab and so fetches chunk (i % 8) ^ (r & 7) of that row; the MFMA fragment reads (row li, chunks
+// g and 4 + g, lanes in groups of 8 rows) are then bank-conflict free.
+// The MFMA runs with the weight as its first operand, so a lane's accumulator holds 4 consecutive
+// output columns of one row: the block-scale fold takes one a_scale per row tile, fp32 partials go
+// out as 16-byte stores, and a lane pair (lane, lane +- 16) swaps halves so that every lane stores
+// 8 consecutive 16-bit outputs.
+// Buffer descriptors start at the workgroup's own tile, so 32-bit offsets cover any matrix size.
+constexpr int kLdsGroup = 8;  // tile rows per raster group
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
+__device__ __forceinline__ uint32_t rsrc_bytes(int64_t bytes) {
+  return (uint32_t)(bytes > 0x7FFFFFFFll ? 0x7FFFFFFFll : (bytes < 0 ? 0 : bytes));
+}
 
-template <int FMT, bool PRE>
-__global__ __launch_bounds__(256) void gemm8_tile_kernel(Gemm8Args p) {
-  __shared__ __attribute__((aligned(16))) uint8_t sA[2][kTileM * 128];
-  __shared__ __attribute__((aligned(16))) uint8_t sB[2][kTileN * 128];
-  __shared__ __attribute__((aligned(16))) float sSA[2][kTileM];
+__device__ __forceinline__ uint32_t pack_out2(float a, float b, int out_dtype) {
+  return out_dtype == AKLR_OUT_BF16 ? (f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16))
+                                    : (f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16));
+}
+
+template <int TM, int TN, int S, int FMT, bool PRE>
+__global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
+  static_assert(TM % 64 == 0 && TN % 128 == 0 && S >= 2, "tile shape");
+  constexpr int MT = TM / 32, NT = TN / 64;  // 16x16 tiles per wave along m and n
+  constexpr int AI = TM / 64, BI = TN / 64;  // 1 KiB loads per wave per stage
+  constexpr int kLoads = AI + BI + 1;        // + one a_scale load
+  constexpr int kStageA = TM * 128, kStageB = TN * 128;
+  constexpr int kScaleWaves = TM / 64;       // waves whose a_scale load carries rows
+  __shared__ __attribute__((aligned(1024))) uint8_t sA[S * kStageA];
+  __shared__ __attribute__((aligned(1024))) uint8_t sB[S * kStageB];
+  __shared__ __attribute__((aligned(16))) float sS[S * TM];
+  __shared__ __attribute__((aligned(16))) float sDummy[8 * 64];  // landing area of the empty a_scale loads
+  __shared__ float sSB[TN / 128][512];  // b_scale of the tile's 128-column blocks over its K range
   __shared__ unsigned arrive_slot;
 
-  const int tiles_m = (p.m + kTileM - 1) / kTileM;
-  const int tiles_n = (p.n + kTileN - 1) / kTileN;
+  const int tiles_m = (p.m + TM - 1) / TM;
+  const int tiles_n = (p.n + TN - 1) / TN;
   // XCD-aware order (the K splits of one tile are consecutive, so they share an XCD and its L2),
-  // then groups of 8 tile-rows so neighbouring tiles share A rows and B columns.
+  // then groups of kLdsGroup tile rows so neighbouring tiles share A rows and B columns.
   const int lid = (int)xcd_remap(blockIdx.x, gridDim.x);
   const int pid = lid / p.splits, split = lid % p.splits;
-  constexpr int kGroup = 8;
-  const int per_group = kGroup * tiles_n;
-  const int group = pid / per_group;
-  const int first_m = group * kGroup;
-  const int gsize = min(tiles_m - first_m, kGroup);
+  const int per_group = kLdsGroup * tiles_n;
+  const int first_m = (pid / per_group) * kLdsGroup;
+  const int gsize = min(tiles_m - first_m, kLdsGroup);
   const int pm = first_m + (pid % per_group) % gsize;
   const int pn = (pid % per_group) / gsize;
-  const int m0 = pm * kTileM, n0 = pn * kTileN;
+  const int m0 = pm * TM, n0 = pn * TN;
 
-  const int t = threadIdx.x;
-  const int lane = t & 63, w = t >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 15, g = lane >> 4;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w >> 2, wn = w & 3;
+  const int KB = p.k >> 7;
   const int kb_begin = split * p.kb_per_split;
-  const int kb_end = min(p.k >> 7, kb_begin + p.kb_per_split);
+  const int kb_end = min(KB, kb_begin + p.kb_per_split);
   const int64_t kt32 = p.k >> 5;
 
-  // global -> register staging
-  const int lc = t & 7, lr = t >> 3;  // chunk and first row this thread moves
-  u32x4 ra[4], rb[4];
-  float rsa = 0.0f;
-  auto gload = [&](int kb) {
+  // Wave w moves rows [w*TM/8, (w+1)*TM/8) of the A tile and [w*TN/8, (w+1)*TN/8) of the B tile in
+  // slabs of 8 rows; waves below kScaleWaves move a_scale rows [64w, 64w + 64), the others issue an
+  // empty load so that every wave's count per stage is kLoads.
+  const i32x4 ars = make_rsrc_words(p.a + (int64_t)m0 * p.lda, rsrc_bytes((int64_t)(p.m - 1 - m0) * p.lda + p.k));
+  const int64_t b_base = PRE ? (int64_t)(n0 >> 4) * kt32 * 512 : (int64_t)n0 * p.ldb;
+  const int64_t b_total = PRE ? (int64_t)p.n * p.k : (int64_t)(p.n - 1) * p.ldb + p.k;
+  const i32x4 brs = make_rsrc_words(p.b + b_base, rsrc_bytes(b_total - b_base));
+  const i32x4 sars = make_rsrc_words(
+      p.sa + (int64_t)m0 * p.sa_sm,
+      rsrc_bytes(((int64_t)(p.m - 1 - m0) * p.sa_sm + (int64_t)(KB - 1) * p.sa_sk + 1) * 4));
+  const int lr = lane >> 3, lp = lane & 7;  // row within the slab, LDS chunk position
+  const int c = lp ^ lr;                     // every slab starts at a multiple of 8 rows
+  uint32_t a_off[AI], b_off[BI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = m0 + lr + 32 * i;
-      ra[i] = row < p.m ? ld16(p.a + (int64_t)row * p.lda + (int64_t)kb * 128 + lc * 16) : u32x4{0, 0, 0, 0};
-    }
-    if (PRE) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int lin = i * 4096 + t * 16;
-        const int rt = lin >> 11, off = lin & 2047;
-        const int64_t tile_row = (n0 >> 4) + rt;
-        rb[i] = (n0 + rt * 16) < p.n ? ld16(p.b + (tile_row * kt32 + (int64_t)kb * 4) * 512 + off)
-                                     : u32x4{0, 0, 0, 0};
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int col = n0 + lr + 32 * i;
-        rb[i] = col < p.n ? ld16(p.b + (int64_t)col * p.ldb + (int64_t)kb * 128 + lc * 16) : u32x4{0, 0, 0, 0};
-      }
-    }
-    if (t < kTileM) {
-      const int row = m0 + t;
-      rsa = row < p.m ? p.sa[(int64_t)row * p.sa_sm + (int64_t)kb * p.sa_sk] : 0.0f;
-    }
-  };
-  auto lstore = [&](int st) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&sA[st][swz(lr + 32 * i, lc)]) = ra[i];
-    if (PRE) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int lin = i * 4096 + t * 16;
-        const int rt = lin >> 11, off = lin & 2047;
-        const int kt = off >> 9, h = (off >> 8) & 1, r = (off >> 4) & 15;
-        *reinterpret_cast<u32x4*>(&sB[st][swz(rt * 16 + r, kt * 2 + h)]) = rb[i];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&sB[st][swz(lr + 32 * i, lc)]) = rb[i];
-    }
-    if (t < kTileM) sSA[st][t] = rsa;
-  };
-
-  f32x4 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const float* sbrow = p.sb + (int64_t)(n0 >> 7) * p.ldbs;
-
-  gload(kb_begin);
-  lstore(0);
-  __syncthreads();
-  for (int kb = kb_begin; kb < kb_end; ++kb) {
-    const int st = (kb - kb_begin) & 1;
-    if (kb + 1 < kb_end) gload(kb + 1);
-    const float sb = sbrow[kb];
-    i32x8 bf[4];
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const int row = wn * 64 + nt * 16 + li;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(&sB[st][swz(row, g)]);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(&sB[st][swz(row, 4 + g)]);
-      bf[nt] = cat(lo, hi);
-    }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int row = wm * 64 + mt * 16 + li;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(&sA[st][swz(row, g)]);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(&sA[st][swz(row, 4 + g)]);
-      const i32x8 af = cat(lo, hi);
-      const f32x4 sa4 = *reinterpret_cast<const f32x4*>(&sSA[st][wm * 64 + mt * 16 + 4 * g]);
-      f32x4 s4;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s4[r] = sa4[r] * sb;
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        const f32x4 part = mfma16x128<FMT>(af, bf[nt], z);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(part[r], s4[r], acc[mt][nt][r]);
-      }
-    }
-    if (kb + 1 < kb_end) lstore(st ^ 1);
-    __syncthreads();
+  for (int j = 0; j < AI; ++j) {
+    const int r = w * (TM / 8) + j * 8 + lr;
+    a_off[j] = m0 + r < p.m ? (uint32_t)(r * p.lda + c * 16) : kOobOffset;
   }
+#pragma unroll
+  for (int j = 0; j < BI; ++j) {
+    const int r = w * (TN / 8) + j * 8 + lr;
+    if (PRE)
+      b_off[j] = n0 + r < p.n ? (uint32_t)((((r >> 4) * kt32 + (c >> 1)) * 512) + (c & 1) * 256 + (r & 15) * 16)
+                              : kOobOffset;
+    else
+      b_off[j] = n0 + r < p.n ? (uint32_t)(r * p.ldb + c * 16) : kOobOffset;
+  }
+  const bool scale_wave = w < kScaleWaves;
+  const uint32_t sa_off =
+      scale_wave && m0 + w * 64 + lane < p.m ? (uint32_t)((w * 64 + lane) * p.sa_sm * 4) : kOobOffset;
+  const uint32_t lds_a = lds_addr(&sA[w * (TM / 8) * 128]), lds_b = lds_addr(&sB[w * (TN / 8) * 128]);
+  const uint32_t lds_s = scale_wave ? lds_addr(&sS[w * 64]) : lds_addr(&sDummy[w * 64]);
+  const uint32_t lds_s_step = scale_wave ? TM * 4 : 0;
+  auto issue = [&](int kb, int st) {
+    const bool on = kb < kb_end;
+    const uint32_t ak = (uint32_t)kb * 128u, bk = PRE ? (uint32_t)kb * 2048u : (uint32_t)kb * 128u;
+#pragma unroll
+    for (int j = 0; j < AI; ++j) lds_dma16(ars, lds_a + st * kStageA + j * 1024, on ? a_off[j] + ak : kOobOffset);
+#pragma unroll
+    for (int j = 0; j < BI; ++j) lds_dma16(brs, lds_b + st * kStageB + j * 1024, on ? b_off[j] + bk : kOobOffset);
+    lds_dma4(sars, lds_s + st * lds_s_step,
+             on && sa_off != kOobOffset ? sa_off + (uint32_t)(kb * p.sa_sk * 4) : kOobOffset);
+  };
 
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // b_scale goes through LDS: a global load inside the loop (after its barriers) could not use the
+  // scalar unit and would be waited for together with the in-flight tile loads.
+  {
+    const int len = kb_end - kb_begin;
+    const int last_row = (p.n - 1) >> 7;
+    for (int i = threadIdx.x; i < (TN / 128) * len; i += 512) {
+      const int r = i / len, kk = i - r * len;
+      sSB[r][kk] = p.sb[(int64_t)min((n0 >> 7) + r, last_row) * p.ldbs + kb_begin + kk];
+    }
+  }
+  const float* sbw = sSB[(wn * (TN / 4)) >> 7];
+
+  // Fragment addresses: every row a lane reads is congruent to li mod 8, so the swizzle term is the
+  // same for all its row tiles and each read is one base plus an immediate (tile * 2048 bytes).
+  const int swz_lo = (g ^ (li & 7)) << 4, swz_hi = ((4 + g) ^ (li & 7)) << 4;
+  const int a_row = (wm * (TM / 2) + li) * 128, b_row = (wn * (TN / 4) + li) * 128;
+  const int s_row = wm * (TM / 2) + li;
+  auto compute = [&](int kb, int st) {
+    const float sb = sbw[kb - kb_begin];
+    const uint8_t* A = sA + st * kStageA;
+    const uint8_t* B = sB + st * kStageB;
+    const float* SA = sS + st * TM + s_row;
+    i32x8 bf[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      bf[nt] = cat(*reinterpret_cast<const u32x4*>(B + b_row + swz_lo + nt * 2048),
+                   *reinterpret_cast<const u32x4*>(B + b_row + swz_hi + nt * 2048));
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const i32x8 af = cat(*reinterpret_cast<const u32x4*>(A + a_row + swz_lo + mt * 2048),
+                           *reinterpret_cast<const u32x4*>(A + a_row + swz_hi + mt * 2048));
+      const float s = SA[mt * 16] * sb;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 part = mfma16x128<FMT>(bf[nt], af, z);  // lane: row li, columns 4g..4g+3
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(part[r], s, acc[mt][nt][r]);
+      }
+    }
+  };
+
+  // Stage kb lives in slot (kb - kb_begin) % S. At each step this wave's loads of the stage about to
+  // be computed are waited for (S - 2 younger stages stay in flight), then the barrier makes every
+  // wave's loads visible and guarantees that no wave still reads the slot the next issue refills
+  // (the slot computed one step earlier). Issues past the end of the K range are empty loads, which
+  // keep the wait count exact.
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s) issue(kb_begin + s, s);
+  int st = 0, st_fill = S - 1;
+  for (int kb = kb_begin; kb < kb_end; ++kb) {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((S - 2) * kLoads) : "memory");
+    __syncthreads();
+    issue(kb + S - 1, st_fill);
+    compute(kb, st);
+    st = st + 1 == S ? 0 : st + 1;
+    st_fill = st_fill + 1 == S ? 0 : st_fill + 1;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  const int row_w = m0 + wm * (TM / 2) + li;  // + mt * 16: the lane's output row
+  const int col_w = n0 + wn * (TN / 4) + 4 * g;  // + nt * 16: the lane's first output column
   if (p.splits > 1) {
-    const int64_t m4 = round4(p.m);
-    const int64_t plane = (int64_t)p.n * m4;
+    // partials: [split][m][n] fp32; a lane stores its 4 columns of one row as one 16-byte access
+    const int64_t plane = (int64_t)p.m * p.n;
     const rsrc_t prs = partial_rsrc(p.partial, split, plane);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const int col = n0 + wn * 64 + nt * 16 + li;
-        const int row0 = m0 + wm * 64 + mt * 16 + 4 * g;
-        if (col < p.n && row0 < p.m) store_partial4(prs, (int64_t)col * m4 + row0, acc[mt][nt]);
+      for (int nt = 0; nt < NT; ++nt) {
+        const int row = row_w + mt * 16, col = col_w + nt * 16;
+        if (row < p.m && col < p.n) store_partial4(prs, (int64_t)row * p.n + col, acc[mt][nt]);
       }
     if (!splitk_arrive(p.counters + pid, p.splits, &arrive_slot)) return;
+    // Sum in split order, one split at a time, with all MT * NT loads of a split in flight together.
+    // Out-of-range positions read the out-of-range offset (zeros) and are never stored.
+    uint32_t poff[MT][NT];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const int col = n0 + wn * 64 + nt * 16 + li;
-        const int row0 = m0 + wm * 64 + mt * 16 + 4 * g;
-        if (col >= p.n || row0 >= p.m) continue;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        for (int sp = 0; sp < p.splits; ++sp) v += load_partial4(partial_rsrc(p.partial, sp, plane), (int64_t)col * m4 + row0);
-        const float bv = p.bias ? p.bias[col] : 0.0f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (row0 + r < p.m) store_out(p.out, (int64_t)(row0 + r) * p.ldo + col, v[r] + bv, p.out_dtype);
+      for (int nt = 0; nt < NT; ++nt) {
+        const int row = row_w + mt * 16, col = col_w + nt * 16;
+        poff[mt][nt] = row < p.m && col < p.n ? (uint32_t)(((int64_t)row * p.n + col) * 4) : kOobOffset;
+        acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-    return;
+    for (int sp = 0; sp < p.splits; ++sp) {
+      const rsrc_t r = partial_rsrc(p.partial, sp, plane);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          acc[mt][nt] += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)poff[mt][nt], 0, kSc1));
+    }
   }
 
+  // Output: for each pair of column tiles (nt, nt + 1) a lane packs its 4 columns of each into two
+  // words, and permlane16_swap exchanges the odd lane groups of the first with the even lane groups
+  // of the second: lane group g then holds columns 8 * (g / 2) .. + 7 of tile nt + (g & 1).
+  const int col_s = n0 + wn * (TN / 4) + (g & 1) * 16 + (g >> 1) * 8;  // + nt * 16 (nt even)
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const int col = n0 + wn * 64 + nt * 16 + li;
-      if (col >= p.n) continue;
-      const float bv = p.bias ? p.bias[col] : 0.0f;
+  for (int nt = 0; nt < NT; nt += 2) {
+    f32x4 bx = {0.f, 0.f, 0.f, 0.f}, by = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias) {
+      const int cx = min(col_w + nt * 16, p.n - 4), cy = min(col_w + nt * 16 + 16, p.n - 4);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * 64 + mt * 16 + 4 * g + r;
-        if (row < p.m) store_out(p.out, (int64_t)row * p.ldo + col, acc[mt][nt][r] + bv, p.out_dtype);
+        bx[r] = p.bias[cx + r];
+        by[r] = p.bias[cy + r];
       }
     }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const f32x4 x = acc[mt][nt] + bx, y = acc[mt][nt + 1] + by;
+      const uint32_t x0 = pack_out2(x[0], x[1], p.out_dtype), x1 = pack_out2(x[2], x[3], p.out_dtype);
+      const uint32_t y0 = pack_out2(y[0], y[1], p.out_dtype), y1 = pack_out2(y[2], y[3], p.out_dtype);
+      const auto s0 = __builtin_amdgcn_permlane16_swap(x0, y0, false, false);
+      const auto s1 = __builtin_amdgcn_permlane16_swap(x1, y1, false, false);
+      const u32x4 v = {s0[0], s1[0], s0[1], s1[1]};
+      const int row = row_w + mt * 16, col = col_s + nt * 16;
+      if (row < p.m && col < p.n)
+        *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + col) = v;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
 // host-side planning
 
-// m <= kSkinnyMaxM streams the weight through the skinny kernel; larger m runs the MFMA tile kernel.
+// m <= kSkinnyMaxM streams the weight through the skinny kernel; larger m runs the LDS kernel.
 static constexpr int64_t kSkinnyMaxM = 64;
 
+enum class Kernel8 { kSkinny, kLds };
+
 struct Plan8 {
-  bool skinny;
+  Kernel8 kind;
   int mt, nt, nw;    // skinny: 16-row and 16-column tiles per wave, waves per workgroup
-  int grid_x;        // skinny: column groups; tile: output tiles
+  int tm, tn;        // lds: workgroup tile
+  int grid_x;        // skinny: column groups; lds: output tiles
   int splits, kb_per_split;
 };
+
+static void finish_splits(Plan8& p, int64_t KB, int64_t s) {
+  if (s < 1 || p.grid_x > kSplitkMaxTiles) s = 1;  // one counter per output tile must fit the region
+  p.kb_per_split = (int)((KB + s - 1) / s);
+  p.splits = (int)((KB + p.kb_per_split - 1) / p.kb_per_split);
+}
+
+// LDS plan for a given tile and split count. s = 0 picks it: 128x128 tiles split K into as many
+// parts as fill one 512-thread workgroup per CU (at most 4, >= 4 K blocks each); the larger tiles do
+// not split (measured: their partials, 2-4x larger, cost more than the parallelism gains).
+static Plan8 plan8_lds(int64_t m, int64_t n, int64_t k, int tm, int tn, int64_t s = 0) {
+  Plan8 p;
+  p.kind = Kernel8::kLds;
+  p.mt = p.nt = p.nw = 0;
+  p.tm = tm;
+  p.tn = tn;
+  const int64_t KB = k / 128;
+  const int64_t tiles = ((m + tm - 1) / tm) * ((n + tn - 1) / tn);
+  p.grid_x = (int)tiles;
+  if (s <= 0) {
+    s = tiles >= 256 || tm + tn > 256 ? 1 : 256 / tiles;
+    if (s > 4) s = 4;
+    if (s > KB / 4) s = KB / 4;
+  }
+  finish_splits(p, KB, s);
+  return p;
+}
+
+// Estimated time (us) of an LDS plan, fitted to MI355X measurements over the DeepSeek-V3 shapes at
+// m = 128..8192 (it picks the fastest measured plan, or one within 2% of it, on all of them): per K
+// block of one tile (256x256: 1.96, 256x128 and 128x256: 1.15, 128x128: 0.70), rounds of 256
+// workgroups, a fixed 3 us per round, and for a K split the partial traffic (s * tile * 4 bytes,
+// stored and then summed by one workgroup at ~100 GB/s) plus 3 us.
+static double lds_cost(const Plan8& p, int64_t k) {
+  const double step = p.tm + p.tn == 512 ? 1.96 : (p.tm + p.tn == 384 ? 1.15 : 0.70);
+  const int64_t wgs = (int64_t)p.grid_x * p.splits;
+  const double rounds = (double)((wgs + 255) / 256);
+  double t = rounds * (p.kb_per_split * step + 3.0);
+  if (p.splits > 1) t += 3.0 + (double)p.splits * p.tm * p.tn * 4 / 100e3;
+  (void)k;
+  return t;
+}
+
+static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
+  static const int kShapes[4][2] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
+  Plan8 best = plan8_lds(m, n, k, 128, 128);
+  double best_t = lds_cost(best, k);
+  for (const auto& sh : kShapes) {
+    if (sh[0] > 128 && m <= 128) continue;  // half of every A tile would be padding
+    const Plan8 p = plan8_lds(m, n, k, sh[0], sh[1]);
+    const double t = lds_cost(p, k);
+    if (t < best_t) {
+      best = p;
+      best_t = t;
+    }
+  }
+  return best;
+}
 
 // Skinny plan (measured on MI355X over the DeepSeek-V3 decode shapes, weights streamed from HBM):
 // one 16-column tile per wave while the activations are a few rows (two once n >= 16384, which
@@ -414,38 +538,22 @@ struct Plan8 {
 // coherent hand-off costs about a kernel launch. Row tiles 1-2 keep two K blocks in flight per
 // wave; four row tiles keep one (their registers would otherwise spill).
 static Plan8 plan8(int64_t m, int64_t n, int64_t k) {
+  if (m > kSkinnyMaxM) return plan8_lds_best(m, n, k);
   Plan8 p;
+  p.kind = Kernel8::kSkinny;
+  p.tm = p.tn = 0;
   const int64_t KB = k / 128;
   int64_t s = 1;
-  if (m <= kSkinnyMaxM) {
-    p.skinny = true;
-    p.mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
-    if (p.mt == 4)
-      p.nt = KB >= 64 ? 4 : 2;
-    else
-      p.nt = m <= 8 ? (n >= 16384 ? 2 : 1) : (m <= 16 ? 2 : 4);
-    const int64_t groups = (n + 16 * p.nt - 1) / (16 * p.nt);
-    p.grid_x = (int)groups;
-    p.nw = (2048 / groups >= 8 && KB >= 16 && !(p.mt == 4 && p.nt == 4)) ? 8 : 4;
-    if (groups * p.nw < 1024 && KB >= 4 * p.nw) s = 2;
-  } else {
-    p.skinny = false;
-    p.mt = p.nt = p.nw = 0;
-    const int64_t tiles = ((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN);
-    p.grid_x = (int)tiles;
-    // Split K when the tiles alone leave CUs idle: aim at 2 workgroups per CU (512), keep at least 4
-    // K blocks per split, and keep the fp32 partials within the weight's own bytes.
-    if (tiles < 512) {
-      s = (512 + tiles - 1) / tiles;
-      int64_t s_max = KB / 4;
-      const int64_t s_traffic = k / (8 * m);
-      if (s_traffic < s_max) s_max = s_traffic;
-      if (s > s_max) s = s_max;
-    }
-  }
-  if (s < 1 || p.grid_x > kSplitkMaxTiles) s = 1;  // one counter per output tile must fit the region
-  p.kb_per_split = (int)((KB + s - 1) / s);
-  p.splits = (int)((KB + p.kb_per_split - 1) / p.kb_per_split);
+  p.mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+  if (p.mt == 4)
+    p.nt = KB >= 64 ? 4 : 2;
+  else
+    p.nt = m <= 8 ? (n >= 16384 ? 2 : 1) : (m <= 16 ? 2 : 4);
+  const int64_t groups = (n + 16 * p.nt - 1) / (16 * p.nt);
+  p.grid_x = (int)groups;
+  p.nw = (2048 / groups >= 8 && KB >= 16 && !(p.mt == 4 && p.nt == 4)) ? 8 : 4;
+  if (groups * p.nw < 1024 && KB >= 4 * p.nw) s = 2;
+  finish_splits(p, KB, s);
   return p;
 }
 
@@ -483,9 +591,20 @@ static void dispatch_skinny(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   else launch_skinny<4, 2, 4, FMT, PRE>(a, d, s);
 }
 
+// Ring depth per tile shape: as many stages as 160 KiB of LDS holds.
+template <int TM, int TN, int FMT, bool PRE>
+static void launch_lds_t(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
+  constexpr int S = TM + TN == 512 ? 2 : (TM + TN == 384 ? 3 : 4);
+  hipLaunchKernelGGL((gemm8_lds_kernel<TM, TN, S, FMT, PRE>), dim3((unsigned)(t.grid_x * t.splits)), dim3(512), 0, s,
+                     a);
+}
+
 template <int FMT, bool PRE>
-static void launch_tile(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
-  hipLaunchKernelGGL((gemm8_tile_kernel<FMT, PRE>), dim3((unsigned)(t.grid_x * t.splits)), dim3(256), 0, s, a);
+static void launch_lds(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
+  if (t.tm == 256 && t.tn == 256) launch_lds_t<256, 256, FMT, PRE>(a, t, s);
+  else if (t.tm == 256) launch_lds_t<256, 128, FMT, PRE>(a, t, s);
+  else if (t.tn == 256) launch_lds_t<128, 256, FMT, PRE>(a, t, s);
+  else launch_lds_t<128, 128, FMT, PRE>(a, t, s);
 }
 
 }  // namespace aklr
@@ -514,6 +633,9 @@ extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void*
       (bias && (reinterpret_cast<uintptr_t>(bias) & 3u)))
     return AKLR_ERR_INVALID_ARGUMENT;
   if (lda < k || lda % 16 != 0 || ldo < n || ldo % 8 != 0) return AKLR_ERR_INVALID_ARGUMENT;
+  // Kernels address a tile's rows with 32-bit offsets from the tile's first row.
+  if (lda >= (1 << 23) || (b_layout == AKLR_B_ROW_MAJOR && ldb >= (1 << 23))) return AKLR_ERR_INVALID_ARGUMENT;
+  if (((m - 1) * sa_stride_m + (k / 128 - 1) * sa_stride_k + 1) * 4 > 0x7FFFFFFFll) return AKLR_ERR_INVALID_ARGUMENT;
   if (b_layout == AKLR_B_ROW_MAJOR && (ldb < k || ldb % 16 != 0)) return AKLR_ERR_INVALID_ARGUMENT;
   if (ldbs < k / 128 || sa_stride_m < 0 || sa_stride_k < 0) return AKLR_ERR_INVALID_ARGUMENT;
   if (m == 0) return AKLR_OK;
@@ -549,12 +671,12 @@ extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void*
     g.counters = static_cast<unsigned*>(workspace);
     g.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kSplitkCounterBytes);
   }
-  if (plan.skinny) {
+  if (plan.kind == Kernel8::kSkinny) {
     if (e5) pre ? dispatch_skinny<1, true>(g, plan, stream) : dispatch_skinny<1, false>(g, plan, stream);
     else pre ? dispatch_skinny<0, true>(g, plan, stream) : dispatch_skinny<0, false>(g, plan, stream);
   } else {
-    if (e5) pre ? launch_tile<1, true>(g, plan, stream) : launch_tile<1, false>(g, plan, stream);
-    else pre ? launch_tile<0, true>(g, plan, stream) : launch_tile<0, false>(g, plan, stream);
+    if (e5) pre ? launch_lds<1, true>(g, plan, stream) : launch_lds<1, false>(g, plan, stream);
+    else pre ? launch_lds<0, true>(g, plan, stream) : launch_lds<0, false>(g, plan, stream);
   }
   AKLR_LAUNCH_CHECK();
   return AKLR_OK;

@@ -119,23 +119,24 @@ def test_prefill_b_shuffled(nk):
     _run_and_check(1024, n, k, variant="b_shuffled", rows=48, cols=384, seed=3)
 
 
-@pytest.mark.parametrize("m", [5, 200])
+@pytest.mark.parametrize("m", [5, 200, 700])
 def test_row_major_a_scale_shuffled_b(m):
     _run_and_check(m, 2112, 7168, variant="b_shuffled_row_major_a_scale", seed=11)
 
 
-@pytest.mark.parametrize("m", [7, 300])
+@pytest.mark.parametrize("m", [7, 300, 777])
 def test_mn_scales_bias_fp16(m):
     _run_and_check(m, 2112, 1536, mode="MN", bias=True, out_dtype=torch.float16, seed=21)
 
 
-@pytest.mark.parametrize("m", [16, 256])
+@pytest.mark.parametrize("m", [16, 256, 640])
 def test_e5m2(m):
     _run_and_check(m, 1024, 2048, dtype=torch.float8_e5m2, seed=31)
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 16, 128), (129, 48, 128), (17, 2112, 256), (130, 144, 384),
-                                   (1, 16, 65536), (16, 256, 16384), (33, 64, 8192)])
+                                   (1, 16, 65536), (16, 256, 16384), (33, 64, 8192),
+                                   (513, 2112, 256), (600, 144, 384), (1000, 48, 1024)])
 def test_small_and_ragged(m, n, k):
     _run_and_check(m, n, k, seed=41)
 
