@@ -36,10 +36,25 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
          _c_int, _c_int, _vp, _c_size, _vp],
     ),
+    "aklr_moe_fp8_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "aklr_deepseek_v2_fp8_moe": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
+         ctypes.c_float, _c_int, _vp, _vp, _c_size, _vp],
+    ),
+    "aklr_moe_fp8_route": (
+        _c_int,
+        [_vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, ctypes.c_float, _c_int, _vp, _vp, _vp],
+    ),
+    "aklr_moe_fp8_experts": (
+        _c_int,
+        [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_size, _vp],
+    ),
 }
 
 # enums of include/aklr_amd.h
 AKLR_OK = 0
+AKLR_ERR_INVALID_ARGUMENT, AKLR_ERR_UNSUPPORTED, AKLR_ERR_WORKSPACE, AKLR_ERR_LAUNCH = 1, 2, 3, 4
 FP8_E4M3FN, FP8_E5M2 = 0, 1
 OUT_BF16, OUT_F16 = 0, 1
 B_ROW_MAJOR, B_PRESHUFFLE_16x16 = 0, 1

@@ -111,6 +111,14 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t id, uint32_t total) {
   return (id % kXcd) * (total / kXcd) + id / kXcd;
 }
 
+// Two 16-byte halves -> one 32-byte MFMA operand (lo = bytes 0-15).
+__device__ __forceinline__ i32x8 cat(const u32x4& lo, const u32x4& hi) {
+  i32x8 r;
+  r[0] = (int)lo[0]; r[1] = (int)lo[1]; r[2] = (int)lo[2]; r[3] = (int)lo[3];
+  r[4] = (int)hi[0]; r[5] = (int)hi[1]; r[6] = (int)hi[2]; r[7] = (int)hi[3];
+  return r;
+}
+
 // 16x16x128 F8F6F4 MFMA. FMT: 0 e4m3, 1 e5m2, 4 e2m1 (both operands). Scale bytes are e8m0;
 // 127 is 1.0. D[i][j] for i = 4*(lane/16) + r, j = lane % 16.
 template <int FMT>

@@ -41,13 +41,6 @@ struct Gemm8Args {
   int kb_per_split;
 };
 
-__device__ __forceinline__ i32x8 cat(const u32x4& lo, const u32x4& hi) {
-  i32x8 r;
-  r[0] = (int)lo[0]; r[1] = (int)lo[1]; r[2] = (int)lo[2]; r[3] = (int)lo[3];
-  r[4] = (int)hi[0]; r[5] = (int)hi[1]; r[6] = (int)hi[2]; r[7] = (int)hi[3];
-  return r;
-}
-
 // Offset, in a PRESHUFFLE_16x16 weight with kt32 = k/32 column tiles, of the 16 bytes that MFMA lane
 // group g (0..3) needs for row `col` and K block kb: k = 16g.. (tile 4kb + g/2, half g%2) and
 // k = 64+16g.. (tile 4kb + 2 + g/2). Returns the first; the second is +1024. The 64 lanes of one

@@ -23,17 +23,20 @@ def _bytes(t: torch.Tensor) -> torch.Tensor:
 
 
 def shuffle_weight(w: torch.Tensor, layout=(16, 16)) -> torch.Tensor:
-    """A [rows, cols] 1-byte-element weight (fp8 codes, or packed fp4 bytes) in aiter's
-    shuffle_weight(layout=(16, 16)) order; rows % 16 == 0, cols % 32 == 0."""
+    """A [..., rows, cols] 1-byte-element weight (fp8 codes, or packed fp4 bytes) in aiter's
+    shuffle_weight(layout=(16, 16)) order on the last two dims (per expert for a 3-D MoE weight);
+    rows % 16 == 0, cols % 32 == 0."""
     if tuple(layout) != (16, 16):
         raise ValueError("only the (16, 16) shuffle is defined for these GEMMs")
-    if w.dim() != 2 or w.element_size() != 1:
-        raise ValueError("shuffle_weight takes a 2-D tensor of 1-byte elements")
-    rows, cols = w.shape
+    if w.dim() < 2 or w.element_size() != 1:
+        raise ValueError("shuffle_weight takes a tensor of 1-byte elements with >= 2 dims")
+    lead, (rows, cols) = tuple(w.shape[:-2]), tuple(w.shape[-2:])
     if rows % 16 or cols % 32:
         raise ValueError(f"shuffle_weight needs rows % 16 == 0 and cols % 32 == 0, got {tuple(w.shape)}")
-    x = _bytes(w).reshape(rows // 16, 16, cols // 32, 2, 16).permute(*_PRESHUFFLE_ORDER)
-    out = x.contiguous().view(rows, cols).view(w.dtype)
+    n = len(lead)
+    order = tuple(range(n)) + tuple(n + i for i in _PRESHUFFLE_ORDER)
+    x = _bytes(w).reshape(*lead, rows // 16, 16, cols // 32, 2, 16).permute(*order)
+    out = x.contiguous().view(w.shape).view(w.dtype)
     out.is_shuffled = True
     return out
 

@@ -128,6 +128,62 @@ int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t* b, int64_
                          int64_t ldo, int64_t m, int64_t n, int64_t k, int b_layout, int scale_layout,
                          int out_dtype, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/*
+ * Grouped DeepSeek FP8 MoE (sglang DeepseekV2MoE.forward_normal on one rank): router logits rounded
+ * to bf16, sigmoid scores, grouped top-k (a group scored by its two best biased scores), the shared
+ * expert as a last slot at weight 1, each expert down(silu(gate(x)) * up(x)) with both linears
+ * 128x128-block-scaled FP8 and their inputs quantized per 1x128 at scale amax / 448 (a division),
+ * the slots weighed and summed in slot order.
+ * Replaces: deepseek_v2_fp8_moe kernel ABI `run(hidden_states, router_weight, correction_bias, w1,
+ *   w1_scale, w2, w2_scale, topk, num_expert_group, topk_group, renormalize, scoring_func,
+ *   routed_scaling_factor, out)` (call keys of aklr/plugins/sglang/models/deepseek_v2/contract.py:
+ *   188-320, api.py:35-50), arithmetic aklr/plugins/sglang/models/deepseek_v2/reference.py:146-183;
+ *   the baseline is aiter fused_moe at per_128x128 (deepseek_v2/baseline.py:113-163).
+ * hidden, out: bf16 [tokens, model_dim]. router_weight: bf16 [n_routed, model_dim]. correction_bias:
+ *   bf16 [n_routed]. w1: e4m3fn [n_routed + 1, 2 * inter_dim, model_dim] (gate rows, then up rows;
+ *   the shared expert last), w1_scale fp32 [n_routed + 1, 2 * inter_dim / 128, model_dim / 128];
+ *   w2: e4m3fn [n_routed + 1, model_dim, inter_dim], w2_scale fp32 [n_routed + 1, model_dim / 128,
+ *   inter_dim / 128]. w_layout: ROW_MAJOR or PRESHUFFLE_16x16 (per expert). scoring is sigmoid.
+ * model_dim, inter_dim multiples of 128 (<= 16384); tokens <= 65536; n_routed <= 1024, divisible by
+ *   num_expert_group (<= 64) with >= 2 experts per group; topk <= 63.
+ * Workspace: aklr_moe_fp8_workspace_bytes(tokens, model_dim, inter_dim, n_routed + 1, topk + 1,
+ *   n_routed); no zeroing needed.
+ */
+size_t aklr_moe_fp8_workspace_bytes(int64_t tokens, int64_t model_dim, int64_t inter_dim, int64_t n_experts,
+                                    int64_t slots, int64_t n_router_rows);
+int aklr_deepseek_v2_fp8_moe(const void* hidden, const void* router_weight, const void* correction_bias,
+                             const void* w1, const float* w1_scale, const void* w2, const float* w2_scale,
+                             int64_t tokens, int64_t model_dim, int64_t inter_dim, int64_t n_routed, int topk,
+                             int num_expert_group, int topk_group, int renormalize, float routed_scaling_factor,
+                             int w_layout, void* out, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * The routing step alone: logits bf16 [tokens, n_routed], correction_bias bf16 [n_routed] ->
+ * ids int32 [tokens, slots], weights fp32 [tokens, slots], slots = topk (+ 1 with append_shared,
+ * which sets slot topk to expert n_routed at weight 1). ids are in descending biased score, the
+ * lower index first among equals.
+ * Replaces: the grouped top-k of aklr/plugins/sglang/models/deepseek_v2/reference.py:121-143 (with
+ *   _with_shared_slot :80-89); the baseline calls sglang/aiter's biased_grouped_topk
+ *   (deepseek_v2/baseline.py `_route`).
+ */
+int aklr_moe_fp8_route(const void* logits, const void* correction_bias, int64_t tokens, int64_t n_routed, int topk,
+                       int num_expert_group, int topk_group, int renormalize, float routed_scaling_factor,
+                       int append_shared, int32_t* ids, float* weights, hipStream_t stream);
+
+/*
+ * The experts on a given routing (every slot, the shared one included): out = sum over slots of
+ * weights[t, s] * expert_{ids[t, s]}(hidden[t]); slots whose id is outside [0, n_experts) are skipped.
+ * Replaces: aiter fused_moe(hidden, w1, w2, topk_weights, topk_ids, activation=Silu,
+ *   quant_type=per_128x128, w1_scale, w2_scale) as called by deepseek_v2/baseline.py:152-163;
+ *   arithmetic aklr/plugins/sglang/models/deepseek_v2/reference.py:64-77, :146-160, :178-181.
+ * ids int32 / weights fp32 [tokens, slots]; weights as in aklr_deepseek_v2_fp8_moe with n_experts
+ *   slots. Workspace: aklr_moe_fp8_workspace_bytes(tokens, model_dim, inter_dim, n_experts, slots, 0).
+ */
+int aklr_moe_fp8_experts(const void* hidden, int64_t tokens, int64_t model_dim, int64_t inter_dim, int64_t n_experts,
+                         const int32_t* ids, const float* weights, int64_t slots, const void* w1, const float* w1_scale,
+                         const void* w2, const float* w2_scale, int w_layout, void* out, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -143,3 +143,66 @@ def test_gemm4_variants(as_gpu):
     assert api(torch.zeros((m, 40), dtype=torch.uint8), torch.zeros((n, 40), dtype=torch.uint8),
                torch.zeros((m, 2), dtype=torch.uint8), torch.zeros((n, 2), dtype=torch.uint8),
                operand_format="none:none") is FR.OUT_OF_CONTRACT  # k = 80, not a multiple of 64
+
+
+# ---------------------------------------------------------------------------------------------
+# deepseek_v2_fp8_moe (deepseek_v2/contract.py:188-320)
+def _moe_args(t=4, n_routed=16, d=256, inter=128, shuffled=False):
+    from aklr_amd import layouts as lay
+
+    bf = torch.bfloat16
+    w1, w2 = fp8((n_routed + 1, 2 * inter, d)), fp8((n_routed + 1, d, inter))
+    if shuffled:
+        w1, w2 = lay.shuffle_weight(w1), lay.shuffle_weight(w2)
+    return [torch.zeros((t, d), dtype=bf), torch.zeros((n_routed, d), dtype=bf), torch.zeros((n_routed,), dtype=bf),
+            w1, torch.ones((n_routed + 1, 2 * inter // 128, d // 128)), w2,
+            torch.ones((n_routed + 1, d // 128, inter // 128)), 8, 8, 4, True, "sigmoid", 2.5]
+
+
+@pytest.fixture
+def moe_as_gpu(monkeypatch, native_lib):
+    from aklr_amd import moe as hm
+
+    monkeypatch.setattr(hm, "on_gpu", lambda *t: True)
+
+
+def test_moe_serving_and_variants(moe_as_gpu):
+    info = aklr_amd.deepseek_v2_fp8_moe.serving(*_moe_args())
+    assert info.contract_id == "deepseek_v2_fp8_moe@1.0" and info.variant == "row_major"
+    assert aklr_amd.deepseek_v2_fp8_moe.serving(*_moe_args(shuffled=True)).variant == "shuffled_16x16"
+    glm = _moe_args(n_routed=32)
+    glm[8], glm[9] = 1, 1
+    assert not isinstance(aklr_amd.deepseek_v2_fp8_moe.serving(*glm), FR)
+
+
+@pytest.mark.parametrize("index,value", [(7, 6), (8, 4), (9, 2), (10, False), (11, "softmax"), (12, 1.0)])
+def test_moe_attrs_outside_contract(moe_as_gpu, index, value):
+    args = _moe_args()
+    args[index] = value
+    assert aklr_amd.deepseek_v2_fp8_moe.fallback_reason(*args) is FR.OUT_OF_CONTRACT
+
+
+def test_moe_shapes_and_layouts_outside_contract(moe_as_gpu):
+    args = _moe_args()
+    args[0] = torch.zeros((4, 200), dtype=torch.bfloat16)  # model_dim % 128
+    assert aklr_amd.deepseek_v2_fp8_moe.fallback_reason(*args) is FR.OUT_OF_CONTRACT
+    args = _moe_args()
+    args[3].is_shuffled = True  # w1 shuffled, w2 not: no variant
+    assert aklr_amd.deepseek_v2_fp8_moe.fallback_reason(*args) is FR.OUT_OF_CONTRACT
+    args = _moe_args(n_routed=12)  # 12 experts in 8 groups
+    assert aklr_amd.deepseek_v2_fp8_moe.fallback_reason(*args) is FR.OUT_OF_CONTRACT
+    args = _moe_args()
+    args[4] = torch.ones((17, 1, 2))  # w1_scale rows
+    assert aklr_amd.deepseek_v2_fp8_moe.fallback_reason(*args) is FR.OUT_OF_CONTRACT
+
+
+def test_moe_cpu_tensors_fall_back():
+    assert aklr_amd.deepseek_v2_fp8_moe(*_moe_args()) is FR.OUT_OF_CONTRACT
+
+
+def test_moe_workspace_bytes(native_lib):
+    # DeepSeek-V3 at T=4096: [T, 7168] fp8 codes, 9 slots of h and y, and the small tables
+    b = native_lib.aklr_moe_fp8_workspace_bytes(4096, 7168, 2048, 257, 9, 256)
+    r = 4096 * 9
+    assert b >= r * 7168 * 2 + r * 2048 + 4096 * 7168
+    assert native_lib.aklr_moe_fp8_workspace_bytes(4096, 7000, 2048, 257, 9, 256) == 0
