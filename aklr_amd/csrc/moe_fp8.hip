@@ -6,11 +6,11 @@
 //   router_kernel    logits[T, Er] = bf16(x @ router^T)                          (bf16 MFMA)
 //   route_kernel     ids[T, S], weights[T, S]: sigmoid, grouped top-k, shared slot last
 //   align_kernel     one workgroup: per-expert counts, the rows sorted by expert (stable only per
-//                    expert, which nothing depends on), each row's position, and the table of
-//                    64-row blocks (expert, first row, rows) the GEMMs walk
+//                    expert, which nothing depends on), each row's position, and the tables of
+//                    256-, 128- and 64-row blocks (expert, first row, rows) the GEMMs walk
 //   quant_div_kernel x -> e4m3 per 1 x 128 at scale max(amax / 448, tiny) (a true division, as the
 //                    checkpoint's FP8 scheme quantizes the linears' inputs), scales [D/128, T]
-//   moe_gemm<GATEUP> per (block, 128 columns of the intermediate): rows gathered by token, gate and up
+//   moe_gemm<GATEUP> per block class, per (block, 128 columns of the intermediate): rows gathered by token, gate and up
 //                    weight rows interleaved per 16 so each lane holds both for the same columns;
 //                    epilogue silu(gate) * up -> bf16 -> e4m3 per 1 x 128 (same division) into h
 //   moe_gemm<DOWN>   per (block, 256 output columns): h rows in sorted order -> y (bf16, sorted)
@@ -24,9 +24,14 @@ namespace moe {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kTM = 64;    // routed rows per GEMM block
+// Row-block classes: an expert's rows split into full 256-row blocks and one last block for the
+// remainder, of the smallest class that holds it (64, 128 or 256 rows). Every block streams the
+// expert's weight tile once, so an expert costs ceil(rows / 256) weight reads -- the fewest for tiles
+// of at most 256 rows -- at the price of some padded MFMA rows in the last block.
+constexpr int kClasses = 3;
+constexpr int kMinTM = 64;
+__host__ __device__ constexpr int class_rows(int k) { return k == 0 ? 256 : (k == 1 ? 128 : 64); }
 constexpr int kTN = 256;   // weight rows per GEMM tile
-constexpr int kStages = 3;
 constexpr int kMaxExperts = 2048;  // expert slots the align kernel's LDS holds
 constexpr float kFp32Tiny = 1.17549435e-38f;
 
@@ -210,13 +215,28 @@ __device__ int block_exclusive_scan(int v, int* wsum, int* total) {
   return r;
 }
 
+// Block table: for each class k, expert[k][i], first row[k][i] and rows[k][i] of its blocks, cap
+// entries per class, and count[k].
+struct BlockTable {
+  int32_t* expert;
+  int32_t* row;
+  int32_t* rows;
+  int32_t* count;
+  int cap;
+};
+
+__device__ __forceinline__ int class_blocks(int c, int k) {
+  const int full = c / 256, rem = c - 256 * full;
+  const int last = rem == 0 ? -1 : (rem > 128 ? 0 : (rem > 64 ? 1 : 2));  // class of the remainder block
+  return (k == 0 ? full : 0) + (k == last ? 1 : 0);
+}
+
 __global__ __launch_bounds__(1024) void align_kernel(const int32_t* __restrict__ ids, int R, int S, int E,
                                                      int32_t* __restrict__ row_of, int32_t* __restrict__ sorted_tok,
-                                                     int32_t* __restrict__ blk_expert, int32_t* __restrict__ blk_row,
-                                                     int32_t* __restrict__ blk_rows, int32_t* __restrict__ nblk) {
+                                                     BlockTable bt) {
   __shared__ int cnt[kMaxExperts];
   __shared__ int off[kMaxExperts];
-  __shared__ int boff[kMaxExperts];
+  __shared__ int boff[kClasses][kMaxExperts];
   __shared__ int wsum[16];
   __shared__ int total;
   const int tid = threadIdx.x;
@@ -227,18 +247,21 @@ __global__ __launch_bounds__(1024) void align_kernel(const int32_t* __restrict__
     row_of[i] = (e >= 0 && e < E) ? atomicAdd(&cnt[e], 1) : -1;
   }
   __syncthreads();
-  // two experts per thread: exclusive prefix of rows and of 64-row blocks
+  // two experts per thread: exclusive prefix of rows, then of each class's blocks
   const int e0 = 2 * tid, e1 = 2 * tid + 1;
   const int c0 = e0 < E ? cnt[e0] : 0, c1 = e1 < E ? cnt[e1] : 0;
   const int o = block_exclusive_scan(c0 + c1, wsum, &total);
   if (e0 < kMaxExperts) off[e0] = o;
   if (e1 < kMaxExperts) off[e1] = o + c0;
-  const int b0 = (c0 + kTM - 1) / kTM, b1 = (c1 + kTM - 1) / kTM;
-  const int bo = block_exclusive_scan(b0 + b1, wsum, &total);
-  if (e0 < kMaxExperts) boff[e0] = bo;
-  if (e1 < kMaxExperts) boff[e1] = bo + b0;
+#pragma unroll
+  for (int k = 0; k < kClasses; ++k) {
+    const int b0 = class_blocks(c0, k), b1 = class_blocks(c1, k);
+    const int bo = block_exclusive_scan(b0 + b1, wsum, &total);
+    if (e0 < kMaxExperts) boff[k][e0] = bo;
+    if (e1 < kMaxExperts) boff[k][e1] = bo + b0;
+    if (tid == 0) bt.count[k] = total;
+  }
   __syncthreads();
-  if (tid == 0) *nblk = total;
   for (int i = tid; i < R; i += 1024) {
     const int e = ids[i];
     if (e < 0 || e >= E) continue;
@@ -248,11 +271,19 @@ __global__ __launch_bounds__(1024) void align_kernel(const int32_t* __restrict__
   }
   for (int e = tid; e < E; e += 1024) {
     const int c = cnt[e];
-    for (int b = 0; b * kTM < c; ++b) {
-      const int idx = boff[e] + b;
-      blk_expert[idx] = e;
-      blk_row[idx] = off[e] + b * kTM;
-      blk_rows[idx] = min(kTM, c - b * kTM);
+    int row = off[e], left = c;
+#pragma unroll
+    for (int k = 0; k < kClasses; ++k) {
+      const int nb = class_blocks(c, k);
+      for (int j = 0; j < nb; ++j) {
+        const int idx = k * bt.cap + boff[k][e] + j;
+        const int n = min(class_rows(k), left);
+        bt.expert[idx] = e;
+        bt.row[idx] = row;
+        bt.rows[idx] = n;
+        row += n;
+        left -= n;
+      }
     }
   }
 }
@@ -320,17 +351,19 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
 __device__ __forceinline__ float round_bf16(float v) { return __uint_as_float(f32_to_bf16_bits(v) << 16); }
 
-// 8 waves in 2 (m) x 4 (n), each 32 rows x 64 weight rows (MT = 2, NT = 4 tiles of 16x16); K steps
-// of 128 through a 3-stage direct-to-LDS ring (2 stages in flight), the same swizzled LDS tiles,
-// load schedule and fold as the dense LDS kernel. GATEUP orders the tile's 256 weight rows as
+// TM-row blocks (one class of the block table) x 256 weight rows; 8 waves in 2 (m) x 4 (n), each
+// TM/2 rows x 64 weight rows (MT = TM/32, NT = 4 tiles of 16x16); K steps of 128 through a direct-to-
+// LDS ring of as many stages as LDS holds (3 for TM <= 128, 2 for 256), with the swizzled LDS tiles,
+// load schedule and fold of the dense LDS kernel. GATEUP orders the tile's 256 weight rows as
 // (gate 16, up 16) pairs over 128 intermediate columns, so tiles nt = 2q and 2q + 1 of a wave are
 // the gate and the up of the same 16 columns.
-template <int MODE, bool PRE>
+template <int MODE, bool PRE, int TM>
 __global__ __launch_bounds__(512) void moe_gemm_kernel(MoeGemmArgs p) {
-  constexpr int TM = kTM, TN = kTN, S = kStages;
+  constexpr int TN = kTN, S = TM == 256 ? 2 : 3;
   constexpr int MT = TM / 32, NT = TN / 64;
-  constexpr int BI = TN / 64;
-  constexpr int kLoads = 1 + BI + 1;
+  constexpr int AI = TM / 64, BI = TN / 64;
+  constexpr int kLoads = AI + BI + 1;
+  constexpr int kScaleWaves = TM / 64;
   constexpr int kStageA = TM * 128, kStageB = TN * 128;
   __shared__ __attribute__((aligned(1024))) uint8_t sA[S * kStageA];
   __shared__ __attribute__((aligned(1024))) uint8_t sB[S * kStageB];
@@ -355,16 +388,23 @@ __global__ __launch_bounds__(512) void moe_gemm_kernel(MoeGemmArgs p) {
     const int blk = item % nblk, pn = item / nblk;
     const int e = p.blk_expert[blk], row0 = p.blk_row[blk], rows = p.blk_rows[blk];
 
-    // A: wave w moves tile rows [8w, 8w + 8); wave 0 also moves the tile's 64 a_scale entries.
-    const int ar = w * 8 + lr;
-    int64_t arow = 0;
-    if (ar < rows) arow = MODE == kGateUp ? p.sorted_tok[row0 + ar] : row0 + ar;
+    // A: wave w moves tile rows [w*TM/8, (w+1)*TM/8) in slabs of 8; waves below kScaleWaves also move
+    // a_scale rows [64w, 64w + 64), the others an empty load (same count per wave).
     const i32x4 ars = make_rsrc_words(p.a, (uint32_t)(p.sa_ld * p.K));  // A has sa_ld rows of K codes
-    const uint32_t a_off = ar < rows ? (uint32_t)(arow * p.K + c * 16) : kOobOffset;
+    uint32_t a_off[AI];
+#pragma unroll
+    for (int j = 0; j < AI; ++j) {
+      const int ar = w * (TM / 8) + j * 8 + lr;
+      int64_t arow = 0;
+      if (ar < rows) arow = MODE == kGateUp ? p.sorted_tok[row0 + ar] : row0 + ar;
+      a_off[j] = ar < rows ? (uint32_t)(arow * p.K + c * 16) : kOobOffset;
+    }
+    const bool scale_wave = w < kScaleWaves;
+    const int sr = w * 64 + lane;
     int64_t srow = 0;
-    if (lane < rows) srow = MODE == kGateUp ? p.sorted_tok[row0 + lane] : row0 + lane;
+    if (scale_wave && sr < rows) srow = MODE == kGateUp ? p.sorted_tok[row0 + sr] : row0 + sr;
     const i32x4 sars = make_rsrc_words(p.sa, (uint32_t)((int64_t)KB * p.sa_ld * 4));
-    const uint32_t sa_off = (w == 0 && lane < rows) ? (uint32_t)(srow * 4) : kOobOffset;
+    const uint32_t sa_off = (scale_wave && sr < rows) ? (uint32_t)(srow * 4) : kOobOffset;
     const uint32_t sa_kstep = (uint32_t)(p.sa_ld * 4);
     // B: this expert's weight; wave w moves tile rows [32w, 32w + 32) in 4 slabs of 8.
     const i32x4 brs = make_rsrc_words(p.b + (int64_t)e * p.b_stride, (uint32_t)p.b_stride);
@@ -386,13 +426,15 @@ __global__ __launch_bounds__(512) void moe_gemm_kernel(MoeGemmArgs p) {
       else
         b_off[j] = (uint32_t)((int64_t)wrow * p.K + c * 16);
     }
-    const uint32_t lds_a = lds_addr(&sA[w * 8 * 128]), lds_b = lds_addr(&sB[w * 32 * 128]);
-    const uint32_t lds_s = w == 0 ? lds_addr(&sS[0]) : lds_addr(&sDummy[w * 64]);
-    const uint32_t lds_s_step = w == 0 ? TM * 4 : 0;
+    const uint32_t lds_a = lds_addr(&sA[w * (TM / 8) * 128]), lds_b = lds_addr(&sB[w * 32 * 128]);
+    const uint32_t lds_s = scale_wave ? lds_addr(&sS[w * 64]) : lds_addr(&sDummy[w * 64]);
+    const uint32_t lds_s_step = scale_wave ? TM * 4 : 0;
     auto issue = [&](int kb, int st) {
       const bool on = kb < KB;
       const uint32_t ak = (uint32_t)kb * 128u, bk = PRE ? (uint32_t)kb * 2048u : (uint32_t)kb * 128u;
-      lds_dma16(ars, lds_a + st * kStageA, on && a_off != kOobOffset ? a_off + ak : kOobOffset);
+#pragma unroll
+      for (int j = 0; j < AI; ++j)
+        lds_dma16(ars, lds_a + st * kStageA + j * 1024, on && a_off[j] != kOobOffset ? a_off[j] + ak : kOobOffset);
 #pragma unroll
       for (int j = 0; j < BI; ++j)
         lds_dma16(brs, lds_b + st * kStageB + j * 1024, on && b_off[j] != kOobOffset ? b_off[j] + bk : kOobOffset);
@@ -419,11 +461,11 @@ __global__ __launch_bounds__(512) void moe_gemm_kernel(MoeGemmArgs p) {
       for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int swz_lo = (g ^ (li & 7)) << 4, swz_hi = ((4 + g) ^ (li & 7)) << 4;
-    const int a_row = (wm * 32 + li) * 128, b_row = (wn * 64 + li) * 128;
+    const int a_row = (wm * (TM / 2) + li) * 128, b_row = (wn * 64 + li) * 128;
     auto compute = [&](int kb, int st) {
       const uint8_t* A = sA + st * kStageA;
       const uint8_t* B = sB + st * kStageB;
-      const float* SA = sS + st * TM + wm * 32 + li;
+      const float* SA = sS + st * TM + wm * (TM / 2) + li;
       float sbv[2];
       if (MODE == kGateUp) {
         sbv[0] = sSB[0][kb];
@@ -467,10 +509,9 @@ __global__ __launch_bounds__(512) void moe_gemm_kernel(MoeGemmArgs p) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     if (MODE == kGateUp) {
-      // h = bf16(silu(gate) * up); per row, e4m3 at scale max(amax / 448, tiny) over the tile's 128
-      // columns (the wave's 32 here, the other 3 waves' through LDS).
-      float h[MT][2][4];
-      float amax[MT];
+      // h = bf16(silu(gate) * up), kept in the gate tiles' registers; per row, e4m3 at scale
+      // max(amax / 448, tiny) over the tile's 128 columns (the wave's 32 here, the other 3 waves'
+      // through LDS).
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         float m = 0.0f;
@@ -479,12 +520,11 @@ __global__ __launch_bounds__(512) void moe_gemm_kernel(MoeGemmArgs p) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float v = round_bf16(silu(acc[mt][2 * q][r]) * acc[mt][2 * q + 1][r]);
-            h[mt][q][r] = v;
+            acc[mt][2 * q][r] = v;
             m = fmaxf(m, fabsf(v));
           }
         m = fmaxf(m, __shfl_xor(m, 16));
         m = fmaxf(m, __shfl_xor(m, 32));
-        amax[mt] = m;
         if (g == 0) sAmax[wm][mt][li][wn] = m;
       }
       __syncthreads();
@@ -492,16 +532,15 @@ __global__ __launch_bounds__(512) void moe_gemm_kernel(MoeGemmArgs p) {
       for (int mt = 0; mt < MT; ++mt) {
         const float m = fmaxf(fmaxf(sAmax[wm][mt][li][0], sAmax[wm][mt][li][1]),
                               fmaxf(sAmax[wm][mt][li][2], sAmax[wm][mt][li][3]));
-        (void)amax[mt];
         const float sc = fmaxf(__fdiv_rn(m, 448.0f), kFp32Tiny);
-        const int tr = wm * 32 + mt * 16 + li;
+        const int tr = wm * (TM / 2) + mt * 16 + li;
         if (tr < rows) {
           const int64_t row = row0 + tr;
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
             float cv[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) cv[r] = fminf(fmaxf(__fdiv_rn(h[mt][q][r], sc), -448.0f), 448.0f);
+            for (int r = 0; r < 4; ++r) cv[r] = fminf(fmaxf(__fdiv_rn(acc[mt][2 * q][r], sc), -448.0f), 448.0f);
             const int col = pn * 128 + wn * 32 + q * 16 + 4 * g;
             *reinterpret_cast<uint32_t*>(p.hq + row * p.I + col) = pack4_e4m3(cv[0], cv[1], cv[2], cv[3]);
           }
@@ -523,7 +562,7 @@ __global__ __launch_bounds__(512) void moe_gemm_kernel(MoeGemmArgs p) {
           const auto s0 = __builtin_amdgcn_permlane16_swap(x0, y0, false, false);
           const auto s1 = __builtin_amdgcn_permlane16_swap(x1, y1, false, false);
           const u32x4 v = {s0[0], s1[0], s0[1], s1[1]};
-          const int tr = wm * 32 + mt * 16 + li, col = col_s + nt * 16;
+          const int tr = wm * (TM / 2) + mt * 16 + li, col = col_s + nt * 16;
           if (tr < rows && col < p.N) *reinterpret_cast<u32x4*>(p.y + (int64_t)(row0 + tr) * p.N + col) = v;
         }
     }
@@ -560,6 +599,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
 // host side
 struct Workspace {
   size_t logits, ids, weights, row_of, sorted_tok, blk_expert, blk_row, blk_rows, nblk, xq, xs, hq, hs, y, total;
+  int blk_cap;  // block-table entries per class
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -569,7 +609,9 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 static Workspace layout(int64_t T, int64_t S, int64_t D, int64_t I, int64_t E, int64_t Er) {
   Workspace w{};
   const int64_t R = T * S;
-  const int64_t maxblk = R / kTM + E + 1;
+  const int64_t cap = R / kMinTM + E + 1;
+  const int64_t maxblk = cap * kClasses;
+  w.blk_cap = (int)cap;
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -584,7 +626,7 @@ static Workspace layout(int64_t T, int64_t S, int64_t D, int64_t I, int64_t E, i
   w.blk_expert = take((size_t)maxblk * 4);
   w.blk_row = take((size_t)maxblk * 4);
   w.blk_rows = take((size_t)maxblk * 4);
-  w.nblk = take(4);
+  w.nblk = take(4 * kClasses);
   w.xq = take((size_t)(T * D));
   w.xs = take((size_t)(D / 128 * T * 4));
   w.hq = take((size_t)(R * I));
@@ -614,11 +656,30 @@ static bool dims_ok(int64_t T, int64_t D, int64_t I, int64_t E, int64_t S) {
   return R * D * 2 < 0x7FFFFFFFll && R * I < 0x7FFFFFFFll && T * D < 0x7FFFFFFFll;
 }
 
-template <bool PRE>
-static void launch_gemms(const MoeGemmArgs& gu, const MoeGemmArgs& dn, hipStream_t stream) {
+template <int MODE, bool PRE>
+static void launch_classes(MoeGemmArgs a, const BlockTable& bt, hipStream_t stream) {
   const dim3 grid((unsigned)num_cus());
-  hipLaunchKernelGGL((moe_gemm_kernel<kGateUp, PRE>), grid, dim3(512), 0, stream, gu);
-  hipLaunchKernelGGL((moe_gemm_kernel<kDown, PRE>), grid, dim3(512), 0, stream, dn);
+  a.blk_expert = bt.expert;
+  a.blk_row = bt.row;
+  a.blk_rows = bt.rows;
+  a.nblk = bt.count;
+  hipLaunchKernelGGL((moe_gemm_kernel<MODE, PRE, 256>), grid, dim3(512), 0, stream, a);
+  a.blk_expert += bt.cap;
+  a.blk_row += bt.cap;
+  a.blk_rows += bt.cap;
+  a.nblk += 1;
+  hipLaunchKernelGGL((moe_gemm_kernel<MODE, PRE, 128>), grid, dim3(512), 0, stream, a);
+  a.blk_expert += bt.cap;
+  a.blk_row += bt.cap;
+  a.blk_rows += bt.cap;
+  a.nblk += 1;
+  hipLaunchKernelGGL((moe_gemm_kernel<MODE, PRE, 64>), grid, dim3(512), 0, stream, a);
+}
+
+template <bool PRE>
+static void launch_gemms(const MoeGemmArgs& gu, const MoeGemmArgs& dn, const BlockTable& bt, hipStream_t stream) {
+  launch_classes<kGateUp, PRE>(gu, bt, stream);
+  launch_classes<kDown, PRE>(dn, bt, stream);
 }
 
 // Experts on a routing already in ids/weights ([T, S], slots in [0, E); others are skipped).
@@ -629,18 +690,19 @@ static int run_experts(const uint16_t* hidden, int64_t T, int64_t D, int64_t I, 
   const int64_t R = T * S;
   int32_t* row_of = reinterpret_cast<int32_t*>(ws + L.row_of);
   int32_t* sorted_tok = reinterpret_cast<int32_t*>(ws + L.sorted_tok);
-  int32_t* blk_expert = reinterpret_cast<int32_t*>(ws + L.blk_expert);
-  int32_t* blk_row = reinterpret_cast<int32_t*>(ws + L.blk_row);
-  int32_t* blk_rows = reinterpret_cast<int32_t*>(ws + L.blk_rows);
-  int32_t* nblk = reinterpret_cast<int32_t*>(ws + L.nblk);
+  BlockTable bt;
+  bt.expert = reinterpret_cast<int32_t*>(ws + L.blk_expert);
+  bt.row = reinterpret_cast<int32_t*>(ws + L.blk_row);
+  bt.rows = reinterpret_cast<int32_t*>(ws + L.blk_rows);
+  bt.count = reinterpret_cast<int32_t*>(ws + L.nblk);
+  bt.cap = L.blk_cap;
   uint8_t* xq = ws + L.xq;
   float* xs = reinterpret_cast<float*>(ws + L.xs);
   uint8_t* hq = ws + L.hq;
   float* hs = reinterpret_cast<float*>(ws + L.hs);
   uint16_t* y = reinterpret_cast<uint16_t*>(ws + L.y);
 
-  hipLaunchKernelGGL(align_kernel, dim3(1), dim3(1024), 0, stream, ids, (int)R, (int)S, (int)E, row_of, sorted_tok,
-                     blk_expert, blk_row, blk_rows, nblk);
+  hipLaunchKernelGGL(align_kernel, dim3(1), dim3(1024), 0, stream, ids, (int)R, (int)S, (int)E, row_of, sorted_tok, bt);
   const int64_t qgroups = T * (D / 128);
   hipLaunchKernelGGL(quant_div_kernel, dim3((unsigned)((qgroups + 15) / 16)), dim3(256), 0, stream, hidden, (int)T,
                      (int)D, xq, xs);
@@ -653,10 +715,6 @@ static int run_experts(const uint16_t* hidden, int64_t T, int64_t D, int64_t I, 
   gu.b_stride = 2 * I * D;
   gu.sb = w1s;
   gu.sb_stride = (2 * I / 128) * (D / 128);
-  gu.blk_expert = blk_expert;
-  gu.blk_row = blk_row;
-  gu.blk_rows = blk_rows;
-  gu.nblk = nblk;
   gu.K = (int)D;
   gu.N = (int)(2 * I);
   gu.I = (int)I;
@@ -678,9 +736,9 @@ static int run_experts(const uint16_t* hidden, int64_t T, int64_t D, int64_t I, 
   dn.tiles_n = (int)((D + kTN - 1) / kTN);
   dn.y = y;
   if (w_layout == AKLR_B_PRESHUFFLE_16x16)
-    launch_gemms<true>(gu, dn, stream);
+    launch_gemms<true>(gu, dn, bt, stream);
   else
-    launch_gemms<false>(gu, dn, stream);
+    launch_gemms<false>(gu, dn, bt, stream);
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)T), dim3(256), 0, stream, y, row_of, weights, (int)S, (int)D, out);
   AKLR_LAUNCH_CHECK();
   return AKLR_OK;

@@ -99,13 +99,14 @@ def _zipf_routing(rng, t, n_routed, topk):
 
 
 @pytest.mark.parametrize("shuffled", [False, True])
-@pytest.mark.parametrize("t,n_routed,d,inter", [(1, 16, 256, 256), (40, 16, 256, 128), (130, 8, 384, 384)])
+@pytest.mark.parametrize("t,n_routed,d,inter", [(1, 16, 256, 256), (40, 16, 256, 128), (130, 8, 384, 384),
+                                                  (300, 4, 256, 128), (700, 8, 256, 256)])
 def test_experts_match_oracle(t, n_routed, d, inter, shuffled):
     say(f"moe experts t={t} n_routed={n_routed} d={d} inter={inter} shuffled={shuffled}")
     rng = np.random.default_rng(t * 7 + d)
     w1, s1, w2, s2 = _experts(rng, n_routed + 1, inter, d)
     x = formats.round_to_bf16(rng.normal(size=(t, d)).astype(np.float32))
-    ids, w = _zipf_routing(rng, t, n_routed, min(8, n_routed))
+    ids, w = _zipf_routing(rng, t, n_routed, min(8, n_routed))  # >= 256 rows per busy expert at t >= 300
     tw1, ts1, tw2, ts2 = _dev_weights(w1, s1, w2, s2, shuffled)
     out = aklr_amd.moe_fp8_experts(_bf16(x), tw1, tw2, torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV),
                                    ts1, ts2)
@@ -138,7 +139,7 @@ def test_experts_skip_invalid_ids_and_are_deterministic():
 
 @pytest.mark.parametrize("shuffled", [False, True])
 @pytest.mark.parametrize("t,n_routed,g,tg,d,inter", [(1, 16, 8, 4, 256, 256), (64, 32, 8, 4, 256, 128),
-                                                    (17, 24, 1, 1, 384, 256)])
+                                                    (17, 24, 1, 1, 384, 256), (400, 16, 8, 4, 256, 128)])
 def test_deepseek_v2_fp8_moe_matches_oracle(t, n_routed, g, tg, d, inter, shuffled):
     say(f"deepseek_v2_fp8_moe t={t} n_routed={n_routed} g={g} tg={tg} d={d} inter={inter} shuffled={shuffled}")
     rng = np.random.default_rng(t + n_routed + d)
