@@ -12,7 +12,14 @@ value = whole-step algorithmic bytes / step time, in GB/s (bytes per GEMM: M*K +
 4*ceil(N/128)*K/128 + 2*M*N; per quant: 3.03125*M*K).
 roofline: the dominant kernel, the skinny (decode) GEMM at M=16, (N, K) = (7168, 16384) (117.97 MB per
 launch), timed alone with HIP events on its stream over graph replays; peak 8 TB/s.
-prefill / mxfp4: extra figures (TFLOP/s vs the dense FP8 5.0 PF / MXFP4 10.1 PF peaks) at M=4096.
+roofline.traffic: HBM bytes per launch of that kernel from two rocprofv3 --pmc runs (FETCH_SIZE, then
+WRITE_SIZE) of ``python3 bench.py --probe-traffic``, each scaled by what the counter reads for a plain
+copy of known size in the same run; read from the committed profiles/ summary (null when absent).
+prefill / mxfp4: extra figures (TFLOP/s vs the dense FP8 5.0 PF / MXFP4 10.1 PF peaks): FP8 at
+M in {1024, 4096, 8192}, MXFP4 at M in {1, 4096}.
+moe: the grouped DeepSeek-V3 FP8 MoE experts (256 routed + 1 shared, top-8,
+D=7168, I=2048, e4m3 weights with 128x128 scales) on Zipf(1.1) routing at T in {64, 4096}: time per
+call, touched-weight bytes / time vs 8 TB/s, and TFLOP/s vs 5.0 PF.
 cpu_baseline: the CPU oracle (numpy dequantize + fp32 matmul, the reference check's formula) on a
 bounded sample (decode M=16, the three shapes), timed on the host in the same run.
 """
@@ -134,8 +141,7 @@ def prefill_figures(dev, stream, steps=10):
     from aklr_amd import layouts, workloads
 
     out = []
-    m = 4096
-    for (n, k) in workloads.DEEPSEEK_NK:
+    for m, (n, k) in ((m, nk) for m in workloads.PREFILL_M for nk in workloads.DEEPSEEK_NK):
         x = workloads.activations(m, k, seed=1, device=dev)
         q, s = aklr_amd.per_group_quant_fp8(x)
         b, bs = workloads.blockwise_fp8_weight(n, k, seed=2, device=dev)
@@ -180,6 +186,86 @@ def mxfp4_figures(dev, stream, steps=10):
             out.append(rec)
             del copies
     return out
+
+
+def moe_figures(dev, steps=10):
+    """Config 5: the experts of the grouped MoE on Zipf(1.1) routing (8 distinct routed experts per
+    token plus the shared one), per call, from HIP events over back-to-back calls."""
+    import aklr_amd
+
+    e, d, inter, topk = 256, 7168, 2048, 8
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+
+    def fp8(shape):  # finite e4m3 codes
+        return torch.randint(0, 0x7E, shape, dtype=torch.uint8, device=dev, generator=g).view(torch.float8_e4m3fn)
+
+    w1, w2 = fp8((e + 1, 2 * inter, d)), fp8((e + 1, d, inter))
+    s1 = torch.rand((e + 1, 2 * inter // 128, d // 128), device=dev, generator=g) * 1e-3
+    s2 = torch.rand((e + 1, d // 128, inter // 128), device=dev, generator=g) * 1e-3
+    p = (1.0 / torch.arange(1, e + 1, device=dev, dtype=torch.float64) ** 1.1).float()
+    out = []
+    for t in (64, 4096):
+        x = torch.randn((t, d), device=dev, generator=g).to(torch.bfloat16)
+        ids = torch.multinomial(p.expand(t, e), topk, replacement=False, generator=g).to(torch.int32)
+        ids = torch.cat([ids, torch.full((t, 1), e, dtype=torch.int32, device=dev)], 1)
+        wts = torch.rand((t, topk + 1), device=dev, generator=g)
+        touched = int(torch.unique(ids).numel())
+        for _ in range(2):
+            aklr_amd.moe_fp8_experts(x, w1, w2, wts, ids, s1, s2)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            aklr_amd.moe_fp8_experts(x, w1, w2, wts, ids, s1, s2)
+        end.record()
+        end.synchronize()
+        sec = start.elapsed_time(end) / steps * 1e-3
+        wbytes = touched * (2 * inter * d + d * inter)
+        flops = 2 * t * (topk + 1) * (2 * inter * d + d * inter)
+        out.append({"tokens": t, "ms": round(sec * 1e3, 3), "experts_touched": touched,
+                    "touched_weight_gb": round(wbytes / 1e9, 3),
+                    "gbs": round(wbytes / sec / 1e9, 1), "frac_hbm_peak": round(wbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+                    "tflops": round(flops / sec / 1e12, 1), "frac_fp8_peak": round(flops / sec / 1e12 / FP8_PEAK_TFLOPS, 4)})
+    del w1, w2
+    return out
+
+
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "gemm8_skinny_m16_n7168_k16384_traffic.json")
+
+
+def probe_traffic(dev, stream):
+    """The program the traffic counters are read on: the dominant decode GEMM (M=16, N=7168,
+    K=16384, preshuffled weights, 8 rotating copies, 3 rounds), then a plain 256 MiB copy three times
+    (the calibration: its FETCH_SIZE and WRITE_SIZE should read 256 MiB each)."""
+    import aklr_amd
+    from aklr_amd import layouts, workloads
+
+    m, n, k = 16, 7168, 16384
+    x = workloads.activations(m, k, seed=5, device=dev)
+    q, s = aklr_amd.per_group_quant_fp8(x)
+    copies = []
+    for r in range(8):
+        b, bs = workloads.blockwise_fp8_weight(n, k, seed=100 + r, device=dev)
+        copies.append((layouts.shuffle_weight(b), bs))
+    for _ in range(3):
+        for b, bs in copies:
+            aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s.view(m, k // 128), bs, operand_format="none:preshuffled")
+    src = torch.empty(256 * 2**20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("[bench] traffic probe done", file=sys.stderr, flush=True)
+
+
+def load_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
 
 
 def cpu_baseline():
@@ -231,6 +317,8 @@ def main(argv=None):
     ap.add_argument("--layout", choices=("preshuffled", "row_major"), default="preshuffled")
     ap.add_argument("--no-extras", action="store_true", help="skip the prefill/MXFP4 figures")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--probe-traffic", action="store_true",
+                    help="only run the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -242,6 +330,9 @@ def main(argv=None):
     # default priority
     stream = torch.cuda.Stream(dev)
     torch.cuda.set_stream(stream)
+    if args.probe_traffic:
+        probe_traffic(dev, stream)
+        return 0
     shuffled = args.layout == "preshuffled"
     print(f"[bench] building decode workload ({args.layout})", file=sys.stderr, flush=True)
     step_fn, n_sets, step_bytes, weights, _ = build_decode(dev, shuffled)
@@ -266,15 +357,19 @@ def main(argv=None):
     extras = {}
     if not args.no_extras:
         print("[bench] prefill and MXFP4 figures", file=sys.stderr, flush=True)
-        extras["prefill_fp8_m4096"] = prefill_figures(dev, stream)
+        extras["prefill_fp8"] = prefill_figures(dev, stream)
         torch.cuda.empty_cache()
         extras["mxfp4"] = mxfp4_figures(dev, stream)
+        torch.cuda.empty_cache()
+        print("[bench] MoE (config 5) figures", file=sys.stderr, flush=True)
+        extras["moe_fp8_deepseek_v3"] = moe_figures(dev)
         torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         cpu = cpu_baseline()
 
+    traffic = load_traffic()
     line = {
         "metric": "block-scaled FP8 GEMM decode HBM GB/s (DeepSeek-V3 decode config)",
         "value": round(value, 1),
@@ -302,7 +397,8 @@ def main(argv=None):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": (traffic or {}).get("bytes_per_launch"),
+            "traffic_source": (traffic or {}).get("source"),
             "launch_us": round(t_dom * 1e3, 2),
             "bytes_per_launch": dom_bytes,
         },
