@@ -139,6 +139,12 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, float v, int o
     reinterpret_cast<uint16_t*>(out)[idx] = (uint16_t)f32_to_f16_bits(v);
 }
 
+// Two outputs -> one word of two bf16 / fp16 values (a in the low half).
+__device__ __forceinline__ uint32_t pack_out2(float a, float b, int out_dtype) {
+  return out_dtype == AKLR_OUT_BF16 ? (f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16))
+                                    : (f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16));
+}
+
 // Split-K partials: layout [split][col][m4] fp32 with m4 = m rounded up to 4, so a lane's 4 rows of
 // one column (an MFMA 16x16 accumulator's rows 4g..4g+3) are one 16-byte access and a wave's
 // accesses are contiguous runs. They travel through device-coherent (sc1) buffer accesses, which go

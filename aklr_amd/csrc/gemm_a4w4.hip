@@ -9,8 +9,10 @@
 // * decode (m <= 32): weight streaming, as the FP8 decode kernel -- a workgroup owns 16 columns and a
 //   K range, each wave a contiguous K sub-range; fixed-order wave reduction in LDS, then (when K is
 //   also split across workgroups) fp32 partials in the caller's workspace summed in split order.
-// * tile (m > 32): 128x128 tiles, 4 waves of 64x64, K steps of 256 (128 bytes per row) double-
-//   buffered in LDS with the scale bytes staged beside them.
+// * lds (m > 32, k % 256 == 0): the FP8 LDS kernel's tiles and direct-to-LDS ring, K steps of 256
+//   values with the scale bytes staged beside the codes (see gemm4_lds_kernel).
+// * tile (m > 32, other k): 128x128 tiles, 4 waves of 64x64, K steps of 256 (128 bytes per row)
+//   double-buffered in LDS through registers with the scale bytes staged beside them.
 // K % 64 == 0: a K step reaching past K reads zero codes and unit scales there.
 #include "common.h"
 
@@ -32,8 +34,10 @@ struct Gemm4Args {
   int b_pre, scale_shuffled, out_dtype;
   int64_t pc;  // padded scale columns (shuffled layout)
   float* partial;
+  unsigned* counters;  // lds kernel split-K arrival counters
   int splits;
-  int ks_per_split;  // 128-wide K steps per split
+  int ks_per_split;  // K steps per split: 128 values (decode), 256 values (lds)
+  int pr_a, pr_b;    // padded scale rows (shuffled layout)
 };
 
 __device__ __forceinline__ int64_t scale_offset(int64_t row, int64_t col, int shuffled, int64_t ld, int64_t pc) {
@@ -296,6 +300,226 @@ __global__ __launch_bounds__(256) void gemm4_tile_kernel(Gemm4Args p) {
     }
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// lds (m > 32, k % 256 == 0): the FP8 LDS kernel's design (gemm_a8w8.hip) -- TM x TN tiles of 8
+// waves in 2 (m) x 4 (n), an S-stage direct-to-LDS ring with the same count of loads per wave per
+// stage, the weight as the first MFMA operand so a lane holds 4 columns of one row -- with K steps
+// of 256 values (128 bytes per row, the same XOR-swizzled LDS tiles) feeding two MFMAs each. The
+// e8m0 scales ride the MFMA; they are staged per step beside the codes: TM x 8 and TN x 8 bytes.
+// In aiter's shuffled scale layout the 8 scale columns of a K step and a 32-row block are one
+// contiguous 256-byte chunk, loaded as it is; lane (li, g) then finds its scales for both MFMAs of
+// the step and both 16-row halves in the dword at (16g + li) * 4, byte 2 * mfma + half. Row-major
+// scales are staged as 8 bytes per row (lane pairs load a row's two dwords).
+template <int TM, int TN, int S, bool PRE, bool SSHUF>
+__global__ __launch_bounds__(512) void gemm4_lds_kernel(Gemm4Args p) {
+  static_assert(TM % 64 == 0 && TN % 128 == 0 && S >= 2, "tile shape");
+  constexpr int MT = TM / 32, NT = TN / 64, AI = TM / 64, BI = TN / 64;
+  constexpr int kLoads = AI + BI + 2;  // + one A-scale and one B-scale load
+  constexpr int kStageA = TM * 128, kStageB = TN * 128, kScaleA = TM * 8, kScaleB = TN * 8;
+  __shared__ __attribute__((aligned(1024))) uint8_t sA[S * kStageA];
+  __shared__ __attribute__((aligned(1024))) uint8_t sB[S * kStageB];
+  __shared__ __attribute__((aligned(16))) uint8_t sSA[S * kScaleA];
+  __shared__ __attribute__((aligned(16))) uint8_t sSB[S * kScaleB];
+  __shared__ __attribute__((aligned(16))) uint32_t sDummy[8 * 64];
+  __shared__ unsigned arrive_slot;
+
+  const int tiles_m = (p.m + TM - 1) / TM, tiles_n = (p.n + TN - 1) / TN;
+  const int lid = (int)xcd_remap(blockIdx.x, gridDim.x);
+  const int pid = lid / p.splits, split = lid % p.splits;
+  constexpr int kGroup = 8;
+  const int per_group = kGroup * tiles_n;
+  const int first_m = (pid / per_group) * kGroup;
+  const int gsize = min(tiles_m - first_m, kGroup);
+  const int pm = first_m + (pid % per_group) % gsize;
+  const int pn = (pid % per_group) / gsize;
+  const int m0 = pm * TM, n0 = pn * TN;
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, g = lane >> 4;
+  const int wm = w >> 2, wn = w & 3;
+  const int KS = p.k >> 8;
+  const int ks_begin = split * p.ks_per_split;
+  const int ks_end = min(KS, ks_begin + p.ks_per_split);
+  const int64_t kbytes = p.k >> 1, kt32 = kbytes >> 5;
+
+  auto clamp_bytes = [](int64_t b) { return (uint32_t)(b > 0x7FFFFFFFll ? 0x7FFFFFFFll : (b < 0 ? 0 : b)); };
+  const i32x4 ars = make_rsrc_words(p.a + (int64_t)m0 * p.lda, clamp_bytes((int64_t)(p.m - 1 - m0) * p.lda + kbytes));
+  const int64_t b_base = PRE ? (int64_t)(n0 >> 4) * kt32 * 512 : (int64_t)n0 * p.ldb;
+  const int64_t b_total = PRE ? (int64_t)p.n * kbytes : (int64_t)(p.n - 1) * p.ldb + kbytes;
+  const i32x4 brs = make_rsrc_words(p.b + b_base, clamp_bytes(b_total - b_base));
+  const int lr = lane >> 3, lp = lane & 7;
+  const int c = lp ^ lr;
+  uint32_t a_off[AI], b_off[BI];
+#pragma unroll
+  for (int j = 0; j < AI; ++j) {
+    const int r = w * (TM / 8) + j * 8 + lr;
+    a_off[j] = m0 + r < p.m ? (uint32_t)(r * p.lda + c * 16) : kOobOffset;
+  }
+#pragma unroll
+  for (int j = 0; j < BI; ++j) {
+    const int r = w * (TN / 8) + j * 8 + lr;
+    if (PRE)
+      b_off[j] = n0 + r < p.n ? (uint32_t)((((r >> 4) * kt32 + (c >> 1)) * 512) + (c & 1) * 256 + (r & 15) * 16)
+                              : kOobOffset;
+    else
+      b_off[j] = n0 + r < p.n ? (uint32_t)(r * p.ldb + c * 16) : kOobOffset;
+  }
+  // scales: wave w < TM/32 (TN/32) moves 32 rows' 8 bytes of the step
+  const bool sa_wave = w < TM / 32, sb_wave = w < TN / 32;
+  i32x4 sars, sbrs;
+  uint32_t sa_off, sb_off, sa_step, sb_step;
+  if (SSHUF) {
+    const int64_t c8 = (int64_t)(p.pc >> 3);
+    sars = make_rsrc_words(p.sa, clamp_bytes((int64_t)p.pr_a * p.pc));
+    sbrs = make_rsrc_words(p.sb, clamp_bytes((int64_t)p.pr_b * p.pc));
+    sa_off = sa_wave ? (uint32_t)(((int64_t)(m0 / 32 + w) * c8) * 256 + lane * 4) : kOobOffset;
+    sb_off = sb_wave ? (uint32_t)(((int64_t)(n0 / 32 + w) * c8) * 256 + lane * 4) : kOobOffset;
+    sa_step = sb_step = 256;
+  } else {
+    sars = make_rsrc_words(p.sa, clamp_bytes((int64_t)(p.m - 1) * p.lds_a + (p.k >> 5)));
+    sbrs = make_rsrc_words(p.sb, clamp_bytes((int64_t)(p.n - 1) * p.lds_b + (p.k >> 5)));
+    const int ra = m0 + w * 32 + (lane >> 1), rb = n0 + w * 32 + (lane >> 1);
+    sa_off = sa_wave && ra < p.m ? (uint32_t)((int64_t)ra * p.lds_a + (lane & 1) * 4) : kOobOffset;
+    sb_off = sb_wave && rb < p.n ? (uint32_t)((int64_t)rb * p.lds_b + (lane & 1) * 4) : kOobOffset;
+    sa_step = sb_step = 8;
+  }
+  const uint32_t lds_a = lds_addr(&sA[w * (TM / 8) * 128]), lds_b = lds_addr(&sB[w * (TN / 8) * 128]);
+  const uint32_t lds_sa = sa_wave ? lds_addr(&sSA[w * 256]) : lds_addr(&sDummy[w * 64]);
+  const uint32_t lds_sb = sb_wave ? lds_addr(&sSB[w * 256]) : lds_addr(&sDummy[w * 64]);
+  const uint32_t lds_sa_step = sa_wave ? kScaleA : 0, lds_sb_step = sb_wave ? kScaleB : 0;
+  auto issue = [&](int ks, int st) {
+    const bool on = ks < ks_end;
+    const uint32_t ak = (uint32_t)ks * 128u, bk = PRE ? (uint32_t)ks * 2048u : (uint32_t)ks * 128u;
+#pragma unroll
+    for (int j = 0; j < AI; ++j) lds_dma16(ars, lds_a + st * kStageA + j * 1024, on ? a_off[j] + ak : kOobOffset);
+#pragma unroll
+    for (int j = 0; j < BI; ++j) lds_dma16(brs, lds_b + st * kStageB + j * 1024, on ? b_off[j] + bk : kOobOffset);
+    lds_dma4(sars, lds_sa + st * lds_sa_step, on && sa_off != kOobOffset ? sa_off + (uint32_t)ks * sa_step : kOobOffset);
+    lds_dma4(sbrs, lds_sb + st * lds_sb_step, on && sb_off != kOobOffset ? sb_off + (uint32_t)ks * sb_step : kOobOffset);
+  };
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int a_row = (wm * (TM / 2) + li) * 128, b_row = (wn * (TN / 4) + li) * 128;
+  // scale word addresses: shuffled -> the row block's chunk, dword (16g + li); row-major -> row * 8
+  const int sa_word = SSHUF ? ((wm * (TM / 2)) / 32) * 256 + (16 * g + li) * 4 : (wm * (TM / 2) + li) * 8;
+  const int sb_word = SSHUF ? ((wn * (TN / 4)) / 32) * 256 + (16 * g + li) * 4 : (wn * (TN / 4) + li) * 8;
+  auto compute = [&](int st) {
+    const uint8_t* A = sA + st * kStageA;
+    const uint8_t* B = sB + st * kStageB;
+    const uint8_t* SA = sSA + st * kScaleA + sa_word;
+    const uint8_t* SB = sSB + st * kScaleB + sb_word;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int swz = ((4 * j + g) ^ (li & 7)) << 4;
+      i32x8 bf[NT];
+      int bsc[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        bf[nt] = fp4_frag(*reinterpret_cast<const u32x4*>(B + b_row + swz + nt * 2048));
+        if (SSHUF) {
+          const uint32_t wd = *reinterpret_cast<const uint32_t*>(SB + (nt >> 1) * 256);
+          bsc[nt] = (int)(wd >> (8 * (2 * j + (nt & 1))));
+        } else {
+          const uint32_t wd = *reinterpret_cast<const uint32_t*>(SB + nt * 128 + 4 * j);
+          bsc[nt] = (int)(wd >> (8 * g));
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const i32x8 af = fp4_frag(*reinterpret_cast<const u32x4*>(A + a_row + swz + mt * 2048));
+        int asc;
+        if (SSHUF) {
+          const uint32_t wd = *reinterpret_cast<const uint32_t*>(SA + (mt >> 1) * 256);
+          asc = (int)(wd >> (8 * (2 * j + (mt & 1))));
+        } else {
+          const uint32_t wd = *reinterpret_cast<const uint32_t*>(SA + mt * 128 + 4 * j);
+          asc = (int)(wd >> (8 * g));
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          acc[mt][nt] = mfma16x128_scaled<kFp4, 0, 0>(bf[nt], af, acc[mt][nt], bsc[nt], asc);  // lane: row li, cols 4g..
+      }
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s) issue(ks_begin + s, s);
+  int st = 0, st_fill = S - 1;
+  for (int ks = ks_begin; ks < ks_end; ++ks) {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((S - 2) * kLoads) : "memory");
+    __syncthreads();
+    issue(ks + S - 1, st_fill);
+    compute(st);
+    st = st + 1 == S ? 0 : st + 1;
+    st_fill = st_fill + 1 == S ? 0 : st_fill + 1;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  const int row_w = m0 + wm * (TM / 2) + li;
+  const int col_w = n0 + wn * (TN / 4) + 4 * g;
+  if (p.splits > 1) {
+    const int64_t plane = (int64_t)p.m * p.n;
+    const rsrc_t prs = partial_rsrc(p.partial, split, plane);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int row = row_w + mt * 16, col = col_w + nt * 16;
+        if (row < p.m && col < p.n) store_partial4(prs, (int64_t)row * p.n + col, acc[mt][nt]);
+      }
+    if (!splitk_arrive(p.counters + pid, p.splits, &arrive_slot)) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < p.splits; ++sp) {
+      const rsrc_t r = partial_rsrc(p.partial, sp, plane);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int row = row_w + mt * 16, col = col_w + nt * 16;
+          const uint32_t off = row < p.m && col < p.n ? (uint32_t)(((int64_t)row * p.n + col) * 4) : kOobOffset;
+          acc[mt][nt] += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kSc1));
+        }
+    }
+  }
+
+  // bf16/fp16 out: lane pairs swap halves so every lane stores 8 consecutive outputs (16 bytes)
+  const int col_s = n0 + wn * (TN / 4) + (g & 1) * 16 + (g >> 1) * 8;
+#pragma unroll
+  for (int nt = 0; nt < NT; nt += 2) {
+    f32x4 bx = {0.f, 0.f, 0.f, 0.f}, by = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias) {
+      const int cx = min(col_w + nt * 16, p.n - 4), cy = min(col_w + nt * 16 + 16, p.n - 4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bx[r] = p.bias[cx + r];
+        by[r] = p.bias[cy + r];
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const f32x4 x = acc[mt][nt] + bx, y = acc[mt][nt + 1] + by;
+      const uint32_t x0 = pack_out2(x[0], x[1], p.out_dtype), x1 = pack_out2(x[2], x[3], p.out_dtype);
+      const uint32_t y0 = pack_out2(y[0], y[1], p.out_dtype), y1 = pack_out2(y[2], y[3], p.out_dtype);
+      const auto s0 = __builtin_amdgcn_permlane16_swap(x0, y0, false, false);
+      const auto s1 = __builtin_amdgcn_permlane16_swap(x1, y1, false, false);
+      const u32x4 v = {s0[0], s1[0], s0[1], s1[1]};
+      const int row = row_w + mt * 16, col = col_s + nt * 16;
+      if (row < p.m && col < p.n)
+        *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + col) = v;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 struct Decode4Plan {
   int mt, nw, splits, ks_per_split;
@@ -321,14 +545,86 @@ static Decode4Plan plan_decode4(int64_t m, int64_t n, int64_t k) {
 
 static constexpr int64_t kDecode4MaxM = 32;
 
+// LDS-kernel plan for m > 32 when k % 256 == 0 (and, for row-major scales, 4-byte aligned scale rows):
+// tile and split count by the FP8 LDS kernel's cost model (per-K-step times per tile shape, rounds of
+// 256 workgroups, only 128x128 tiles split K).
+struct Lds4Plan {
+  int tm, tn, tiles, splits, ks_per_split;
+};
+
+static Lds4Plan lds4_plan_for(int64_t m, int64_t n, int64_t k, int tm, int tn) {
+  Lds4Plan p;
+  p.tm = tm;
+  p.tn = tn;
+  const int64_t KS = k / 256;
+  const int64_t tiles = ((m + tm - 1) / tm) * ((n + tn - 1) / tn);
+  p.tiles = (int)tiles;
+  int64_t s = tiles >= 256 || tm + tn > 256 ? 1 : 256 / tiles;
+  if (s > 4) s = 4;
+  if (s > KS / 4) s = KS / 4;
+  if (s < 1 || tiles > kSplitkMaxTiles) s = 1;
+  p.ks_per_split = (int)((KS + s - 1) / s);
+  p.splits = (int)((KS + p.ks_per_split - 1) / p.ks_per_split);
+  return p;
+}
+
+static Lds4Plan plan_lds4(int64_t m, int64_t n, int64_t k) {
+  static const int kShapes[4][2] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
+  Lds4Plan best{};
+  double best_t = 1e30;
+  for (const auto& sh : kShapes) {
+    if (sh[0] > 128 && m <= 128) continue;
+    const Lds4Plan p = lds4_plan_for(m, n, k, sh[0], sh[1]);
+    const double step = p.tm + p.tn == 512 ? 1.96 : (p.tm + p.tn == 384 ? 1.15 : 0.70);
+    const int64_t wgs = (int64_t)p.tiles * p.splits;
+    double t = (double)((wgs + 255) / 256) * (p.ks_per_split * step + 3.0);
+    if (p.splits > 1) t += 3.0 + (double)p.splits * p.tm * p.tn * 4 / 100e3;
+    if (t < best_t) {
+      best = p;
+      best_t = t;
+    }
+  }
+  return best;
+}
+
+static bool lds4_ok(int64_t m, int64_t k, int scale_layout, int64_t lds_a, int64_t lds_b, const uint8_t* sa,
+                    const uint8_t* sb) {
+  if (m <= kDecode4MaxM || k % 256 != 0) return false;
+  if (scale_layout == AKLR_SCALES_ROW_MAJOR &&
+      (lds_a % 4 || lds_b % 4 || (reinterpret_cast<uintptr_t>(sa) & 3u) || (reinterpret_cast<uintptr_t>(sb) & 3u)))
+    return false;
+  return true;
+}
+
+template <int TM, int TN, bool PRE, bool SSHUF>
+static void launch_lds4_t(const Gemm4Args& g, const Lds4Plan& p, hipStream_t s) {
+  constexpr int S = TM + TN == 512 ? 2 : (TM + TN == 384 ? 3 : 4);
+  hipLaunchKernelGGL((gemm4_lds_kernel<TM, TN, S, PRE, SSHUF>), dim3((unsigned)(p.tiles * p.splits)), dim3(512), 0, s, g);
+}
+
+template <bool PRE, bool SSHUF>
+static void launch_lds4(const Gemm4Args& g, const Lds4Plan& p, hipStream_t s) {
+  if (p.tm == 256 && p.tn == 256) launch_lds4_t<256, 256, PRE, SSHUF>(g, p, s);
+  else if (p.tm == 256) launch_lds4_t<256, 128, PRE, SSHUF>(g, p, s);
+  else if (p.tn == 256) launch_lds4_t<128, 256, PRE, SSHUF>(g, p, s);
+  else launch_lds4_t<128, 128, PRE, SSHUF>(g, p, s);
+}
+
 }  // namespace aklr
 
 using namespace aklr;
 
+// Workspace: kSplitkCounterBytes of arrival counters (the LDS kernel's split-K), then fp32 partials
+// [splits, m, n]. The LDS kernel may be declined at call time (row-major scales with unaligned rows),
+// so the size covers whichever path could run.
 extern "C" size_t aklr_gemm_a4w4_mxfp4_workspace_bytes(int64_t m, int64_t n, int64_t k) {
-  if (m <= 0 || n <= 0 || k < 64 || m > kDecode4MaxM) return 0;
-  const Decode4Plan d = plan_decode4(m, n, k);
-  return d.splits > 1 ? (size_t)d.splits * (size_t)m * (size_t)n * sizeof(float) : 0;
+  if (m <= 0 || n <= 0 || k < 64) return 0;
+  int splits = 1;
+  if (m <= kDecode4MaxM)
+    splits = plan_decode4(m, n, k).splits;
+  else if (k % 256 == 0)
+    splits = plan_lds4(m, n, k).splits;
+  return splits > 1 ? kSplitkCounterBytes + (size_t)splits * (size_t)m * (size_t)n * sizeof(float) : 0;
 }
 
 extern "C" int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb,
@@ -369,17 +665,20 @@ extern "C" int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t
   g.out_dtype = out_dtype;
   g.pc = (k / 32 + 7) / 8 * 8;
   g.partial = nullptr;
+  g.counters = nullptr;
   g.splits = 1;
   g.ks_per_split = (int)((k + 127) / 128);
+  g.pr_a = (int)((m + 255) / 256 * 256);
+  g.pr_b = (int)((n + 255) / 256 * 256);
 
   if (m <= kDecode4MaxM) {
     const Decode4Plan d = plan_decode4(m, n, k);
     g.splits = d.splits;
     g.ks_per_split = d.ks_per_split;
     if (d.splits > 1) {
-      const size_t need = (size_t)d.splits * (size_t)m * (size_t)n * sizeof(float);
+      const size_t need = kSplitkCounterBytes + (size_t)d.splits * (size_t)m * (size_t)n * sizeof(float);
       if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) return AKLR_ERR_WORKSPACE;
-      g.partial = static_cast<float*>(workspace);
+      g.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kSplitkCounterBytes);
     }
     dim3 grid((unsigned)(n / 16), (unsigned)d.splits);
     if (d.mt == 1 && d.nw == 8) hipLaunchKernelGGL((gemm4_decode_kernel<1, 8>), grid, dim3(512), 0, stream, g);
@@ -393,6 +692,22 @@ extern "C" int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t
                          g.partial, d.splits, g.m, g.n, bias, out, ldo, out_dtype);
       AKLR_LAUNCH_CHECK();
     }
+    return AKLR_OK;
+  }
+  if (lds4_ok(m, k, scale_layout, lds_a, lds_b, a_scale, b_scale)) {
+    const Lds4Plan lp = plan_lds4(m, n, k);
+    g.splits = lp.splits;
+    g.ks_per_split = lp.ks_per_split;
+    if (lp.splits > 1) {
+      const size_t need = kSplitkCounterBytes + (size_t)lp.splits * (size_t)m * (size_t)n * sizeof(float);
+      if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) return AKLR_ERR_WORKSPACE;
+      g.counters = static_cast<unsigned*>(workspace);
+      g.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kSplitkCounterBytes);
+    }
+    const bool sshuf = scale_layout == AKLR_SCALES_SHUFFLED;
+    if (g.b_pre) sshuf ? launch_lds4<true, true>(g, lp, stream) : launch_lds4<true, false>(g, lp, stream);
+    else sshuf ? launch_lds4<false, true>(g, lp, stream) : launch_lds4<false, false>(g, lp, stream);
+    AKLR_LAUNCH_CHECK();
     return AKLR_OK;
   }
   const int tiles = (int)(((m + kT4M - 1) / kT4M) * ((n + kT4N - 1) / kT4N));

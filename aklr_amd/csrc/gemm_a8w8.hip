@@ -231,11 +231,6 @@ __device__ __forceinline__ uint32_t rsrc_bytes(int64_t bytes) {
   return (uint32_t)(bytes > 0x7FFFFFFFll ? 0x7FFFFFFFll : (bytes < 0 ? 0 : bytes));
 }
 
-__device__ __forceinline__ uint32_t pack_out2(float a, float b, int out_dtype) {
-  return out_dtype == AKLR_OUT_BF16 ? (f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16))
-                                    : (f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16));
-}
-
 template <int TM, int TN, int S, int FMT, bool PRE>
 __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   static_assert(TM % 64 == 0 && TN % 128 == 0 && S >= 2, "tile shape");
@@ -408,13 +403,28 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
         poff[mt][nt] = row < p.m && col < p.n ? (uint32_t)(((int64_t)row * p.n + col) * 4) : kOobOffset;
         acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-    for (int sp = 0; sp < p.splits; ++sp) {
-      const rsrc_t r = partial_rsrc(p.partial, sp, plane);
+    // Splits go in batches of up to kBatch whose loads are all issued before any is added (each
+    // coherent load costs a trip to the memory side); slots past the last split load zeros.
+    constexpr int kBatch = MT * NT <= 8 ? 4 : 1;  // only 128x128 tiles split K (plan8_lds)
+    for (int sp0 = 0; sp0 < p.splits; sp0 += kBatch) {
+      f32x4 v[kBatch][MT][NT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int b = 0; b < kBatch; ++b) {
+        const bool on = sp0 + b < p.splits;
+        const rsrc_t r = partial_rsrc(p.partial, on ? sp0 + b : 0, plane);
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          acc[mt][nt] += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)poff[mt][nt], 0, kSc1));
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            v[b][mt][nt] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, on ? (int)poff[mt][nt] : (int)kOobOffset, 0, kSc1));
+      }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) acc[mt][nt] += v[b][mt][nt];
     }
   }
 

@@ -193,10 +193,21 @@ def test_mxfp4_llama(m, nk, shuffled):
     _mxfp4_run(m, n, k, shuffled, seed=m)
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 16, 64), (3, 32, 192), (33, 48, 320), (200, 272, 64), (40, 160, 4160)])
+@pytest.mark.parametrize("m,n,k", [(1, 16, 64), (3, 32, 192), (33, 48, 320), (200, 272, 64), (40, 160, 4160),
+                                   (33, 48, 256), (129, 16, 512), (300, 272, 1024), (700, 400, 2048),
+                                   (2100, 1040, 768)])
 def test_mxfp4_small_and_ragged_k(m, n, k):
     _mxfp4_run(m, n, k, shuffled=True, seed=m, bias=True)
     _mxfp4_run(m, n, k, shuffled=False, seed=m + 1)
+
+
+@pytest.mark.parametrize("m,n,k", [(100, 272, 512), (1500, 160, 1024), (40, 2048, 8192)])
+def test_mxfp4_lds_split_k_and_determinism(m, n, k):
+    # shapes whose LDS plan splits K (few 128x128 tiles, long K): results equal the oracle and repeat bitwise
+    out1 = _mxfp4_run(m, n, k, shuffled=True, seed=m + 3)
+    out2 = _mxfp4_run(m, n, k, shuffled=True, seed=m + 3)
+    torch.cuda.synchronize()
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
 
 
 def test_quant_gemm_pipeline_matches_oracle_end_to_end():
