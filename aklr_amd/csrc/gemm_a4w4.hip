@@ -6,9 +6,10 @@
 // scale of that row and 32-block, and the atom applies the scales itself. No VALU fold: the MFMA
 // accumulates straight into the fp32 result.
 //
-// * decode (m <= 32): weight streaming, as the FP8 decode kernel -- a workgroup owns 16 columns and a
-//   K range, each wave a contiguous K sub-range; fixed-order wave reduction in LDS, then (when K is
-//   also split across workgroups) fp32 partials in the caller's workspace summed in split order.
+// * skinny (m <= 32): weight streaming, as the FP8 skinny kernel -- a workgroup owns 32 columns and a
+//   K range, each wave a contiguous K sub-range with a register ring; fixed-order wave reduction in
+//   LDS, then (when K is also split across workgroups) fp32 partials summed in split order by the
+//   last workgroup to arrive.
 // * lds (m > 32, k % 256 == 0): the FP8 LDS kernel's tiles and direct-to-LDS ring, K steps of 256
 //   values with the scale bytes staged beside the codes (see gemm4_lds_kernel).
 // * tile (m > 32, other k): 128x128 tiles, 4 waves of 64x64, K steps of 256 (128 bytes per row)
@@ -57,12 +58,38 @@ __device__ __forceinline__ i32x8 fp4_frag(const u32x4& v) {
 constexpr int kFp4 = 4;
 
 // ---------------------------------------------------------------------------------------------
-template <int MT, int NW>
-__global__ __launch_bounds__(NW * 64) void gemm4_decode_kernel(Gemm4Args p) {
-  __shared__ f32x4 red[(NW - 1) * MT * 64];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+// skinny (m <= 32): weight streaming, the FP8 skinny kernel's design (gemm_a8w8.hip). A workgroup owns
+// 16 * NT output columns and a K range (split across workgroups when the columns alone leave the chip
+// idle); each of its NW waves streams its own contiguous sub-range of 128-value K steps straight from
+// HBM into MFMA operand registers through raw buffer loads, a D-deep register ring, steps past the
+// range (or lane groups past k) loading zeros through the out-of-range offset. The e8m0 scales ride
+// the MFMA: shuffled scales come as the dword of the row's 2 x 2 (K step, 16-row half) bytes, shifted
+// to the one needed; row-major ones as single bytes. Waves are summed in LDS in wave order; K splits
+// go through fp32 partials and the arrival counters, the last workgroup summing in split order.
+template <int MT, int NT>
+struct Skinny4Frag {
+  u32x4 a[MT];
+  u32x4 b[NT];
+  uint32_t sa[MT];
+  uint32_t sb[NT];
+};
+
+__device__ __forceinline__ uint32_t buf_ld4(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_ld1(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
+}
+
+template <int MT, int NT, int NW, int D, bool PRE, bool SSHUF>
+__global__ __launch_bounds__(NW * 64) void gemm4_skinny_kernel(Gemm4Args p) {
+  constexpr int T = MT * NT;
+  __shared__ f32x4 red[T][64];
+  __shared__ unsigned arrive_slot;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 16 * NT;
   const int split = blockIdx.y;
   const int KS = (p.k + 127) >> 7;
   const int ks_base = split * p.ks_per_split;
@@ -70,87 +97,141 @@ __global__ __launch_bounds__(NW * 64) void gemm4_decode_kernel(Gemm4Args p) {
   const int chunk = (ks_len + NW - 1) / NW;
   const int ks_begin = ks_base + min(w * chunk, ks_len);
   const int ks_end = ks_base + min((w + 1) * chunk, ks_len);
-  const int64_t kbytes = p.k >> 1;
-  const int64_t kt32 = kbytes >> 5;
-  const int64_t kb32 = p.k >> 5;
+  const int64_t kbytes = p.k >> 1, kt32 = kbytes >> 5;
+  const int kcols = p.k >> 5;  // scale columns
+  const int64_t c8 = p.pc >> 3;
 
-  const int64_t col = n0 + li;
-  const uint8_t* bp = p.b_pre ? p.b + ((col >> 4) * kt32 + (g >> 1)) * 512 + (g & 1) * 256 + (col & 15) * 16
-                              : p.b + col * p.ldb + g * 16;
-  const int64_t bstep = p.b_pre ? 1024 : 64;
-
-  f32x4 acc[MT];
+  rsrc_t brs[NT];
+  int64_t bcol[NT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int nt = 0; nt < NT; ++nt) {
+    const int64_t c0 = (n0 + nt * 16) < p.n ? n0 + nt * 16 : 0;  // tiles past n read tile 0, never stored
+    bcol[nt] = c0 + li;
+    if (PRE)
+      brs[nt] = make_rsrc(p.b + (c0 >> 4) * kt32 * 512, (uint32_t)(kt32 * 512));
+    else
+      brs[nt] = make_rsrc(p.b + c0 * p.ldb, (uint32_t)(15 * p.ldb + kbytes));
+  }
+  const uint32_t b_lane = PRE ? (uint32_t)((g >> 1) * 512 + (g & 1) * 256 + li * 16) : (uint32_t)(li * p.ldb + g * 16);
+  const uint32_t b_step = PRE ? 1024u : 64u;
+  const rsrc_t ars = make_rsrc(p.a, (uint32_t)((p.m - 1) * p.lda + kbytes));
+  uint32_t a_lane[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int row = mt * 16 + li;
+    a_lane[mt] = row < p.m ? (uint32_t)(row * p.lda + g * 16) : kOobOffset;
+  }
+  // scales
+  const rsrc_t sars = SSHUF ? make_rsrc(p.sa, (uint32_t)((int64_t)p.pr_a * p.pc))
+                            : make_rsrc(p.sa, (uint32_t)((p.m - 1) * p.lds_a + kcols));
+  const rsrc_t sbrs = SSHUF ? make_rsrc(p.sb, (uint32_t)((int64_t)p.pr_b * p.pc))
+                            : make_rsrc(p.sb, (uint32_t)((p.n - 1) * p.lds_b + kcols));
+  uint32_t sa_base[MT], sb_base[NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int row = mt * 16 + li;
+    sa_base[mt] = SSHUF ? (uint32_t)(((int64_t)(row >> 5) * c8) * 256 + (g * 16 + (row & 15)) * 4)
+                        : (row < p.m ? (uint32_t)(row * p.lds_a + g) : kOobOffset);
+  }
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    sb_base[nt] = SSHUF ? (uint32_t)(((bcol[nt] >> 5) * c8) * 256 + (g * 16 + (bcol[nt] & 15)) * 4)
+                        : (uint32_t)(bcol[nt] * p.lds_b + g);
 
-  for (int ks = ks_begin; ks < ks_end; ++ks) {
-    const bool kin = (int64_t)ks * 64 + g * 16 < kbytes;  // this lane group's 32 values exist
-    const int64_t c = (int64_t)ks * 4 + g;                  // scale column (32-block)
-    u32x4 bv = {0, 0, 0, 0};
-    int bs = 127;
-    if (kin) {
-      bv = ld16_nt(bp + (int64_t)ks * bstep);
-      bs = p.sb[scale_offset(col, c, p.scale_shuffled, p.lds_b, p.pc)];
+  auto load = [&](int ks, Skinny4Frag<MT, NT>& f) {
+    const bool on = ks < ks_end && (int64_t)ks * 64 + g * 16 < kbytes;  // this lane group's 32 values exist
+    const uint32_t dk = on ? 0u : kOobOffset;
+    const uint32_t so = SSHUF ? (uint32_t)(ks >> 1) * 256u : (uint32_t)ks * 4u;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      f.b[nt] = buf_ld16<kNt>(brs[nt], on ? b_lane + (uint32_t)ks * b_step : kOobOffset);
+      f.sb[nt] = SSHUF ? buf_ld4(sbrs, on ? sb_base[nt] + so : kOobOffset)
+                       : buf_ld1(sbrs, on ? sb_base[nt] + so : kOobOffset);
     }
-    const i32x8 bf = fp4_frag(bv);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int row = mt * 16 + li;
-      u32x4 av = {0, 0, 0, 0};
-      int as = 127;
-      if (kin && row < p.m) {
-        av = ld16(p.a + (int64_t)row * p.lda + (int64_t)ks * 64 + g * 16);
-        as = p.sa[scale_offset(row, c, p.scale_shuffled, p.lds_a, p.pc)];
-      }
-      acc[mt] = mfma16x128_scaled<kFp4, 0, 0>(fp4_frag(av), bf, acc[mt], as, bs);
+      f.a[mt] = buf_ld16(ars, (on && a_lane[mt] != kOobOffset) ? a_lane[mt] + (uint32_t)ks * 64u : kOobOffset);
+      f.sa[mt] = SSHUF ? buf_ld4(sars, on ? sa_base[mt] + so : kOobOffset)
+                       : buf_ld1(sars, (on && sa_base[mt] != kOobOffset) ? sa_base[mt] + so : kOobOffset);
     }
-  }
-  (void)kb32;
+    (void)dk;
+  };
 
-  if (w > 0) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) red[((w - 1) * MT + mt) * 64 + lane] = acc[mt];
-  }
-  __syncthreads();
-  if (w != 0) return;
-#pragma unroll
-  for (int v = 1; v < NW; ++v)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const f32x4 o = red[((v - 1) * MT + mt) * 64 + lane];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[mt][r] += o[r];
-    }
+  f32x4 acc[MT][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = mt * 16 + 4 * g + r;
-      if (row >= p.m) continue;
-      if (p.splits > 1) {
-        p.partial[((int64_t)split * p.m + row) * p.n + col] = acc[mt][r];
-      } else {
-        float v = acc[mt][r];
-        if (p.bias) v += p.bias[col];
-        store_out(p.out, (int64_t)row * p.ldo + col, v, p.out_dtype);
-      }
-    }
-}
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-__global__ __launch_bounds__(256) void gemm4_splitk_reduce_kernel(const float* __restrict__ partial, int splits,
-                                                                  int m, int n, const float* __restrict__ bias,
-                                                                  void* out, int64_t ldo, int out_dtype) {
-  const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-  const int64_t total = (int64_t)m * n;
-  if (idx >= total) return;
-  const int row = (int)(idx / n), col = (int)(idx % n);
-  f32x4 s = *reinterpret_cast<const f32x4*>(partial + idx);
-  for (int sp = 1; sp < splits; ++sp) s += *reinterpret_cast<const f32x4*>(partial + (int64_t)sp * total + idx);
+  Skinny4Frag<MT, NT> f[D];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float v = s[j];
-    if (bias) v += bias[col + j];
-    store_out(out, (int64_t)row * ldo + col + j, v, out_dtype);
+  for (int j = 0; j < D; ++j) load(ks_begin + j, f[j]);
+  for (int ks0 = ks_begin; ks0 < ks_end; ks0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int ks = ks0 + j;
+      // shuffled scales: byte (K step parity) * 2 + (16-row half) of the dword
+      const int kshift = SSHUF ? 16 * (ks & 1) : 0;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int asc = (int)(f[j].sa[mt] >> (kshift + (SSHUF ? 8 * (mt & 1) : 0)));
+        const i32x8 af = fp4_frag(f[j].a[mt]);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int bsc = (int)(f[j].sb[nt] >> (kshift + (SSHUF ? 8 * (int)((bcol[nt] >> 4) & 1) : 0)));
+          acc[mt][nt] = mfma16x128_scaled<kFp4, 0, 0>(af, fp4_frag(f[j].b[nt]), acc[mt][nt], asc, bsc);
+        }
+      }
+      load(ks0 + j + D, f[j]);
+      __builtin_amdgcn_sched_barrier(0);  // refill slot j before consuming slot j + 1
+    }
+  }
+
+  for (int v = 0; v < NW; ++v) {
+    if (w == v) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int t = mt * NT + nt;
+          red[t][lane] = v == 0 ? acc[mt][nt] : red[t][lane] + acc[mt][nt];
+        }
+    }
+    __syncthreads();
+  }
+
+  const int64_t m4 = round4(p.m);
+  const int64_t plane = (int64_t)p.n * m4;
+  for (int t = w; t < T; t += NW) {
+    const int mt = t / NT, nt = t % NT;
+    const int c0 = n0 + nt * 16;
+    if (c0 >= p.n) continue;
+    const f32x4 sv = red[t][lane];
+    const int col = c0 + li;
+    const int row0 = mt * 16 + 4 * g;
+    if (p.splits > 1) {
+      if (row0 < p.m) store_partial4(partial_rsrc(p.partial, split, plane), (int64_t)col * m4 + row0, sv);
+      continue;
+    }
+    const float bv = p.bias ? p.bias[col] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (row0 + r < p.m) store_out(p.out, (int64_t)(row0 + r) * p.ldo + col, sv[r] + bv, p.out_dtype);
+  }
+  if (p.splits == 1) return;
+  if (!splitk_arrive(p.counters + blockIdx.x, p.splits, &arrive_slot)) return;
+  for (int t = w; t < T; t += NW) {
+    const int mt = t / NT, nt = t % NT;
+    const int c0 = n0 + nt * 16;
+    const int row0 = mt * 16 + 4 * g;
+    if (c0 >= p.n || row0 >= p.m) continue;
+    const int col = c0 + li;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < p.splits; ++sp) v += load_partial4(partial_rsrc(p.partial, sp, plane), (int64_t)col * m4 + row0);
+    const float bv = p.bias ? p.bias[col] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (row0 + r < p.m) store_out(p.out, (int64_t)(row0 + r) * p.ldo + col, v[r] + bv, p.out_dtype);
   }
 }
 
@@ -521,29 +602,43 @@ __global__ __launch_bounds__(512) void gemm4_lds_kernel(Gemm4Args p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-struct Decode4Plan {
-  int mt, nw, splits, ks_per_split;
+static constexpr int64_t kDecode4MaxM = 32;
+
+// Skinny plan (m <= 32), measured on MI355X over the Llama-70B MXFP4 shapes at m = 1 and 32: one or
+// two 16-row tiles, two 16-column tiles and 4 waves per workgroup, 2 K steps in flight per wave
+// (best or within 3% of the best of 2-8 in flight, 4 or 8 waves, 1-4 column tiles and 1-4 K splits);
+// K is split in two only when the columns give fewer than 512 waves (small n).
+struct Skinny4Plan {
+  int mt, nt, nw, d, groups, splits, ks_per_split;
 };
 
-static Decode4Plan plan_decode4(int64_t m, int64_t n, int64_t k) {
-  Decode4Plan d;
-  d.mt = m <= 16 ? 1 : 2;
-  const int KS = (int)((k + 127) / 128);
-  d.nw = KS < 16 ? 4 : 8;
-  const int64_t n_tiles = n / 16;
-  int64_t s = (4096 + n_tiles * d.nw - 1) / (n_tiles * d.nw);
-  int64_t s_max = KS / (2 * d.nw);
-  // partial traffic (8 B per output per split) under ~15% of the weight bytes (k/2 + k/32 per column)
-  const int64_t s_traffic = (int64_t)(0.15 * (double)k * 0.53125 / (8.0 * (double)m));
-  if (s_traffic < s_max) s_max = s_traffic;
-  if (s > s_max) s = s_max;
-  if (s < 1) s = 1;
-  d.ks_per_split = (int)((KS + s - 1) / s);
-  d.splits = (int)((KS + d.ks_per_split - 1) / d.ks_per_split);
-  return d;
+static Skinny4Plan plan_skinny4(int64_t m, int64_t n, int64_t k) {
+  Skinny4Plan p;
+  p.mt = m <= 16 ? 1 : 2;
+  const int64_t KS = (k + 127) / 128;
+  p.nt = 2;
+  p.groups = (int)((n + 16 * p.nt - 1) / (16 * p.nt));
+  p.nw = 4;
+  p.d = (p.mt == 1 && KS >= 128) ? 4 : 2;
+  int64_t s = ((int64_t)p.groups * p.nw < 512 && KS >= 16) ? 2 : 1;
+  if (p.groups > kSplitkMaxTiles) s = 1;
+  p.ks_per_split = (int)((KS + s - 1) / s);
+  p.splits = (int)((KS + p.ks_per_split - 1) / p.ks_per_split);
+  return p;
 }
 
-static constexpr int64_t kDecode4MaxM = 32;
+template <int MT, int D, bool PRE, bool SSHUF>
+static void launch_skinny4(const Gemm4Args& g, const Skinny4Plan& p, hipStream_t s) {
+  hipLaunchKernelGGL((gemm4_skinny_kernel<MT, 2, 4, D, PRE, SSHUF>), dim3((unsigned)p.groups, (unsigned)p.splits),
+                     dim3(256), 0, s, g);
+}
+
+template <bool PRE, bool SSHUF>
+static void launch_skinny4(const Gemm4Args& g, const Skinny4Plan& p, hipStream_t s) {
+  if (p.mt == 1 && p.d == 4) launch_skinny4<1, 4, PRE, SSHUF>(g, p, s);
+  else if (p.mt == 1) launch_skinny4<1, 2, PRE, SSHUF>(g, p, s);
+  else launch_skinny4<2, 2, PRE, SSHUF>(g, p, s);
+}
 
 // LDS-kernel plan for m > 32 when k % 256 == 0 (and, for row-major scales, 4-byte aligned scale rows):
 // tile and split count by the FP8 LDS kernel's cost model (per-K-step times per tile shape, rounds of
@@ -621,10 +716,10 @@ extern "C" size_t aklr_gemm_a4w4_mxfp4_workspace_bytes(int64_t m, int64_t n, int
   if (m <= 0 || n <= 0 || k < 64) return 0;
   int splits = 1;
   if (m <= kDecode4MaxM)
-    splits = plan_decode4(m, n, k).splits;
+    splits = plan_skinny4(m, n, k).splits;
   else if (k % 256 == 0)
     splits = plan_lds4(m, n, k).splits;
-  return splits > 1 ? kSplitkCounterBytes + (size_t)splits * (size_t)m * (size_t)n * sizeof(float) : 0;
+  return splits > 1 ? kSplitkCounterBytes + (size_t)splits * (size_t)round4(m) * (size_t)n * sizeof(float) : 0;
 }
 
 extern "C" int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb,
@@ -672,26 +767,19 @@ extern "C" int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t
   g.pr_b = (int)((n + 255) / 256 * 256);
 
   if (m <= kDecode4MaxM) {
-    const Decode4Plan d = plan_decode4(m, n, k);
+    const Skinny4Plan d = plan_skinny4(m, n, k);
     g.splits = d.splits;
     g.ks_per_split = d.ks_per_split;
     if (d.splits > 1) {
-      const size_t need = kSplitkCounterBytes + (size_t)d.splits * (size_t)m * (size_t)n * sizeof(float);
+      const size_t need = kSplitkCounterBytes + (size_t)d.splits * (size_t)round4(m) * (size_t)n * sizeof(float);
       if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) return AKLR_ERR_WORKSPACE;
+      g.counters = static_cast<unsigned*>(workspace);
       g.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kSplitkCounterBytes);
     }
-    dim3 grid((unsigned)(n / 16), (unsigned)d.splits);
-    if (d.mt == 1 && d.nw == 8) hipLaunchKernelGGL((gemm4_decode_kernel<1, 8>), grid, dim3(512), 0, stream, g);
-    else if (d.mt == 1) hipLaunchKernelGGL((gemm4_decode_kernel<1, 4>), grid, dim3(256), 0, stream, g);
-    else if (d.nw == 8) hipLaunchKernelGGL((gemm4_decode_kernel<2, 8>), grid, dim3(512), 0, stream, g);
-    else hipLaunchKernelGGL((gemm4_decode_kernel<2, 4>), grid, dim3(256), 0, stream, g);
+    const bool sshuf = scale_layout == AKLR_SCALES_SHUFFLED;
+    if (g.b_pre) sshuf ? launch_skinny4<true, true>(g, d, stream) : launch_skinny4<true, false>(g, d, stream);
+    else sshuf ? launch_skinny4<false, true>(g, d, stream) : launch_skinny4<false, false>(g, d, stream);
     AKLR_LAUNCH_CHECK();
-    if (d.splits > 1) {
-      const int64_t quads = (m * n) / 4;
-      hipLaunchKernelGGL(gemm4_splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
-                         g.partial, d.splits, g.m, g.n, bias, out, ldo, out_dtype);
-      AKLR_LAUNCH_CHECK();
-    }
     return AKLR_OK;
   }
   if (lds4_ok(m, k, scale_layout, lds_a, lds_b, a_scale, b_scale)) {
