@@ -5,11 +5,14 @@
 // with one FMA per element: acc += partial * (a_scale[row, kb] * b_scale[n/128, kb]). The fp32 block
 // scales are not powers of two, so they cannot ride the MFMA's e8m0 scale operands.
 //
-// * skinny (m <= 64): weight streaming. A workgroup owns 16*NT output columns and a K range; each of
+// * skinny (m <= 16): weight streaming. A workgroup owns 16*NT output columns and a K range; each of
 //   its waves streams its own contiguous K sub-range of the weight straight from HBM into MFMA
 //   operand registers (no LDS), D K-blocks in flight, with the activations from L2. The waves'
 //   accumulators are summed in one LDS tile in wave order.
-// * lds (m > 64): 256x256, 256x128, 128x256 or 128x128 workgroup tiles of 8 waves, K steps of 128
+// * stream (16 < m <= 128): weight streaming with the activations shared through LDS. Each compute
+//   wave streams its own weight columns over the workgroup's K range into a register ring, and a
+//   loader wave fills an LDS ring with each K block of A in MFMA fragment order.
+// * lds (m > 128): 256x256, 256x128, 128x256 or 128x128 workgroup tiles of 8 waves, K steps of 128
 //   through a 2- to 4-stage LDS ring filled by direct-to-LDS loads (16-byte chunks XOR-swizzled by
 //   row), a_scale staged in LDS, XCD-aware tile order, 16-byte output stores.
 //
@@ -36,7 +39,7 @@ struct Gemm8Args {
   int m, n, k;
   int out_dtype;
   unsigned* counters;  // one per output tile when splits > 1
-  float* partial;      // when splits > 1: skinny [splits, n, round4(m)], lds [splits, m, n]
+  float* partial;      // when splits > 1: skinny [splits, n, round4(m)], stream and lds [splits, m, n]
   int splits;
   int kb_per_split;
 };
@@ -212,7 +215,285 @@ __global__ __launch_bounds__(NW * 64) void gemm8_skinny_kernel(Gemm8Args p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// lds (m > 64): TM x TN workgroup tiles, 8 waves in 2 (m) x 4 (n), each wave (TM/2) x (TN/4), K steps
+// stream: weight streaming with the activations shared through LDS, for a few row tiles (MT <= 8).
+// A workgroup owns NW * NT * 16 output columns and a K range. Its NW compute waves own NT 16-column
+// tiles each and stream those weight columns from HBM straight into a D-deep register ring, as the
+// skinny kernel does; one more wave, the loader, moves each 128-wide K block of A (all MT row tiles)
+// and its a_scale column into an NS-stage LDS ring with direct-to-LDS loads, so A crosses L2 once per
+// workgroup instead of once per wave. A lands in MFMA fragment order -- 1 KiB chunk (mt, h) holds at
+// lane l's 16 bytes row mt * 16 + l % 16, bytes 64h + 16 (l / 16) of the block -- and every compute
+// read is one contiguous ds_read_b128.
+// The loader issues only LDS-bound loads and the compute waves only register-bound ones, so both
+// sides' wait counts are exact: the loader waits for its own stage with an immediate count, and the
+// compiler tracks the weight ring. One barrier per K block, fenced for LDS only, hands a stage from
+// the loader to the compute waves and the consumed slot back, without draining the weight ring.
+__device__ __forceinline__ uint32_t rsrc_bytes(int64_t bytes) {
+  return (uint32_t)(bytes > 0x7FFFFFFFll ? 0x7FFFFFFFll : (bytes < 0 ? 0 : bytes));
+}
+
+__device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int NT>
+struct StreamFrag {
+  i32x8 b[NT];
+};
+
+template <int MT, int NT, int NW, int D, int NS, int FMT, bool PRE>
+__global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p) {
+  static_assert(NS >= 2 && D >= 1 && MT >= 1 && MT <= 8 && 128 % (NT * 16) == 0, "stream shape");
+  constexpr int kSRows = (MT * 16 + 63) / 64 * 64;  // a_scale floats per stage: whole 64-lane loads
+  constexpr int kLoadsA = 2 * MT + kSRows / 64;     // loader loads per stage
+  constexpr int kCols = NW * NT * 16;
+  constexpr int kNBlk = kCols >= 128 ? kCols / 128 : 1;  // 128-column b_scale blocks under the workgroup
+  static_assert((NS - 2) * kLoadsA <= 63, "the loader's wait count must fit vmcnt");
+  __shared__ __attribute__((aligned(1024))) uint8_t sA[NS][MT * 2048];
+  __shared__ __attribute__((aligned(16))) float sS[NS][kSRows];
+  __shared__ float sSB[kNBlk][512];
+  __shared__ unsigned arrive_slot;
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * kCols;
+  const int split = blockIdx.y;
+  const int KB = p.k >> 7;
+  const int kb_begin = split * p.kb_per_split;
+  const int kb_end = min(KB, kb_begin + p.kb_per_split);
+  const int64_t kt32 = p.k >> 5;
+
+  // b_scale of the workgroup's column blocks over its K range (kb_per_split <= 512), staged once.
+  {
+    const int len = kb_end - kb_begin;
+    const int last_row = (p.n - 1) >> 7;
+    for (int i = threadIdx.x; i < kNBlk * len; i += (NW + 1) * 64) {
+      const int r = i / len, kk = i - r * len;
+      sSB[r][kk] = p.sb[(int64_t)min((n0 >> 7) + r, last_row) * p.ldbs + kb_begin + kk];
+    }
+  }
+  __syncthreads();
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int c0w = n0 + w * NT * 16;  // compute wave's first column
+  const int col_w = c0w + 4 * g;     // + nt * 16: the lane's first output column
+
+  if (w == NW) {
+    // Loader. Rows past m read the out-of-range offset: zeros, no memory access.
+    const i32x4 ars = make_rsrc_words(p.a, rsrc_bytes((int64_t)(p.m - 1) * p.lda + p.k));
+    const i32x4 sars =
+        make_rsrc_words(p.sa, rsrc_bytes(((int64_t)(p.m - 1) * p.sa_sm + (int64_t)(KB - 1) * p.sa_sk + 1) * 4));
+    uint32_t a_off[MT], s_off[kSRows / 64];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int row = mt * 16 + li;
+      a_off[mt] = row < p.m ? (uint32_t)((int64_t)row * p.lda + g * 16) : kOobOffset;
+    }
+#pragma unroll
+    for (int i = 0; i < kSRows / 64; ++i) {
+      const int row = i * 64 + lane;
+      s_off[i] = row < p.m ? (uint32_t)((int64_t)row * p.sa_sm * 4) : kOobOffset;
+    }
+    const uint32_t lds_a0 = lds_addr(&sA[0][0]), lds_s0 = lds_addr(&sS[0][0]);
+    auto issue = [&](int kb, int st) {
+      const bool on = kb < kb_end;
+      const uint32_t ak = (uint32_t)kb * 128u, sk = (uint32_t)kb * (uint32_t)(p.sa_sk * 4);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          lds_dma16(ars, lds_a0 + st * (MT * 2048) + mt * 2048 + h * 1024,
+                    on && a_off[mt] != kOobOffset ? a_off[mt] + ak + 64 * h : kOobOffset);
+#pragma unroll
+      for (int i = 0; i < kSRows / 64; ++i)
+        lds_dma4(sars, lds_s0 + st * (kSRows * 4) + i * 256, on && s_off[i] != kOobOffset ? s_off[i] + sk : kOobOffset);
+    };
+    // Stage kb lives in slot (kb - kb_begin) % NS. Before barrier kb the loader's own loads of stage
+    // kb have landed (NS - 2 younger stages stay in flight); after it, every compute wave is done with
+    // stage kb - 1, whose slot the next issue refills. Issues past the K range load zeros, which keeps
+    // the count exact.
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) issue(kb_begin + s, s);
+    int st_fill = NS - 1;
+    for (int kb = kb_begin; kb < kb_end; ++kb) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * kLoadsA) : "memory");
+      stage_barrier();
+      issue(kb + NS - 1, st_fill);
+      st_fill = st_fill + 1 == NS ? 0 : st_fill + 1;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    // Compute wave. Column tiles past n read tile 0: they feed only outputs that are never stored.
+    rsrc_t brs[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int64_t c0 = (c0w + nt * 16) < p.n ? c0w + nt * 16 : 0;
+      if (PRE)
+        brs[nt] = make_rsrc(p.b + (c0 >> 4) * kt32 * 512, (uint32_t)(kt32 * 512));
+      else
+        brs[nt] = make_rsrc(p.b + c0 * p.ldb, (uint32_t)(15 * p.ldb + p.k));
+    }
+    const uint32_t b_lane = PRE ? (uint32_t)((g >> 1) * 512 + (g & 1) * 256 + li * 16)
+                                : (uint32_t)(li * p.ldb + g * 16);
+    auto load = [&](int kb, StreamFrag<NT>& f) {
+      const uint32_t boff = kb < kb_end ? (uint32_t)(PRE ? kb * 2048 : kb * 128) : kOobOffset;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        f.b[nt] = cat(buf_ld16<kNt>(brs[nt], b_lane + boff), buf_ld16<kNt>(brs[nt], b_lane + boff + (PRE ? 1024 : 64)));
+    };
+    const float* sbw = sSB[(c0w >> 7) - (n0 >> 7)];
+
+    // One K block: all MT fragment reads of the stage are issued before the first MFMA, so their LDS
+    // latency overlaps; then the weight slot is refilled with block kb + D.
+    int st = 0;
+    auto step = [&](int kb, StreamFrag<NT>& f) {
+      stage_barrier();
+      const float sb = sbw[kb - kb_begin];
+      const uint8_t* A = sA[st];
+      const float* SA = sS[st];
+      i32x8 af[MT];
+      float s[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        af[mt] = cat(*reinterpret_cast<const u32x4*>(A + mt * 2048 + lane * 16),
+                     *reinterpret_cast<const u32x4*>(A + mt * 2048 + 1024 + lane * 16));
+        s[mt] = SA[mt * 16 + li];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const float sc = s[mt] * sb;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+          const f32x4 part = mfma16x128<FMT>(f.b[nt], af[mt], z);  // lane: row li, columns 4g..4g+3
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(part[r], sc, acc[mt][nt][r]);
+        }
+      }
+      load(kb + D, f);
+      __builtin_amdgcn_sched_barrier(0);  // refill this slot before consuming the next
+      st = st + 1 == NS ? 0 : st + 1;
+    };
+
+    // D-deep ring: block kb_begin + i lives in slot i % D. Whole groups of D blocks run in a loop with
+    // no exit inside (its head then has one ring state, and the compiler waits for exactly the slot
+    // it consumes); the remaining < D blocks follow, one guarded step each.
+    StreamFrag<NT> f[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) load(kb_begin + j, f[j]);
+    const int len = kb_end - kb_begin, full = len / D * D;
+    for (int kb0 = kb_begin; kb0 < kb_begin + full; kb0 += D) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) step(kb0 + j, f[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < D - 1; ++j)
+      if (full + j < len) step(kb_begin + full + j, f[j]);
+    if (p.splits > 1) {
+      // partials: [split][m][n] fp32; a lane stores its 4 columns of one row as one 16-byte access
+      const rsrc_t prs = partial_rsrc(p.partial, split, (int64_t)p.m * p.n);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int row = mt * 16 + li, col = col_w + nt * 16;
+          if (row < p.m && col < p.n) store_partial4(prs, (int64_t)row * p.n + col, acc[mt][nt]);
+        }
+    }
+  }
+
+  if (p.splits > 1) {
+    if (!splitk_arrive(p.counters + blockIdx.x, p.splits, &arrive_slot)) return;
+    if (w == NW) return;
+    // Sum in split order, each split's MT * NT loads in flight together; positions past m or n read
+    // the out-of-range offset (zeros) and are never stored.
+    const int64_t plane = (int64_t)p.m * p.n;
+    uint32_t poff[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int row = mt * 16 + li, col = col_w + nt * 16;
+        poff[mt][nt] = row < p.m && col < p.n ? (uint32_t)(((int64_t)row * p.n + col) * 4) : kOobOffset;
+        acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    for (int sp = 0; sp < p.splits; ++sp) {
+      const rsrc_t r = partial_rsrc(p.partial, sp, plane);
+      f32x4 v[MT][NT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          v[mt][nt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)poff[mt][nt], 0, kSc1));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] += v[mt][nt];
+    }
+  }
+  if (w == NW) return;
+
+  // Output. Even NT: for each pair of column tiles a lane packs its 4 columns of each into two words
+  // and permlane16_swap exchanges the odd lane groups of the first with the even lane groups of the
+  // second, so lane group g stores columns 8 * (g / 2) .. + 7 of tile nt + (g & 1) as 16 bytes.
+  // NT = 1: each lane stores its 4 columns as 8 bytes.
+  if constexpr (NT % 2 == 0) {
+    const int col_s = c0w + (g & 1) * 16 + (g >> 1) * 8;  // + nt * 16 (nt even)
+#pragma unroll
+    for (int nt = 0; nt < NT; nt += 2) {
+      f32x4 bx = {0.f, 0.f, 0.f, 0.f}, by = {0.f, 0.f, 0.f, 0.f};
+      if (p.bias) {
+        const int cx = min(col_w + nt * 16, p.n - 4), cy = min(col_w + nt * 16 + 16, p.n - 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          bx[r] = p.bias[cx + r];
+          by[r] = p.bias[cy + r];
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const f32x4 x = acc[mt][nt] + bx, y = acc[mt][nt + 1] + by;
+        const uint32_t x0 = pack_out2(x[0], x[1], p.out_dtype), x1 = pack_out2(x[2], x[3], p.out_dtype);
+        const uint32_t y0 = pack_out2(y[0], y[1], p.out_dtype), y1 = pack_out2(y[2], y[3], p.out_dtype);
+        const auto s0 = __builtin_amdgcn_permlane16_swap(x0, y0, false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(x1, y1, false, false);
+        const u32x4 v = {s0[0], s1[0], s0[1], s1[1]};
+        const int row = mt * 16 + li, col = col_s + nt * 16;
+        if (row < p.m && col < p.n)
+          *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + col) = v;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int col = col_w + nt * 16;
+      if (col >= p.n) continue;
+      f32x4 bx = {0.f, 0.f, 0.f, 0.f};
+      if (p.bias) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bx[r] = p.bias[col + r];
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int row = mt * 16 + li;
+        if (row >= p.m) continue;
+        const f32x4 x = acc[mt][nt] + bx;
+        const u32x2 v = {pack_out2(x[0], x[1], p.out_dtype), pack_out2(x[2], x[3], p.out_dtype)};
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + col) = v;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// lds (m > 128): TM x TN workgroup tiles, 8 waves in 2 (m) x 4 (n), each wave (TM/2) x (TN/4), K steps
 // of 128 through an S-stage LDS ring that S - 1 stages fill ahead of the compute. A, B and a_scale go
 // global -> LDS with direct-to-LDS buffer loads (no register staging), every wave issuing the same
 // number of loads per stage, so one immediate wait count leaves exactly S - 2 stages in flight.
@@ -226,10 +507,6 @@ __global__ __launch_bounds__(NW * 64) void gemm8_skinny_kernel(Gemm8Args p) {
 // 8 consecutive 16-bit outputs.
 // Buffer descriptors start at the workgroup's own tile, so 32-bit offsets cover any matrix size.
 constexpr int kLdsGroup = 8;  // tile rows per raster group
-
-__device__ __forceinline__ uint32_t rsrc_bytes(int64_t bytes) {
-  return (uint32_t)(bytes > 0x7FFFFFFFll ? 0x7FFFFFFFll : (bytes < 0 ? 0 : bytes));
-}
 
 template <int TM, int TN, int S, int FMT, bool PRE>
 __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
@@ -461,16 +738,18 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
 // ---------------------------------------------------------------------------------------------
 // host-side planning
 
-// m <= kSkinnyMaxM streams the weight through the skinny kernel; larger m runs the LDS kernel.
-static constexpr int64_t kSkinnyMaxM = 64;
+// m <= kSkinnyMaxM streams the weight through the skinny kernel, m <= kStreamMaxM through the stream
+// kernel (activations shared in LDS); larger m runs the LDS kernel.
+static constexpr int64_t kSkinnyMaxM = 16;
+static constexpr int64_t kStreamMaxM = 128;
 
-enum class Kernel8 { kSkinny, kLds };
+enum class Kernel8 { kSkinny, kStream, kLds };
 
 struct Plan8 {
   Kernel8 kind;
-  int mt, nt, nw;    // skinny: 16-row and 16-column tiles per wave, waves per workgroup
+  int mt, nt, nw;    // skinny, stream: 16-row and 16-column tiles per wave, waves per workgroup
   int tm, tn;        // lds: workgroup tile
-  int grid_x;        // skinny: column groups; lds: output tiles
+  int grid_x;        // skinny, stream: column groups; lds: output tiles
   int splits, kb_per_split;
 };
 
@@ -532,32 +811,53 @@ static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
   return best;
 }
 
-// Skinny plan (measured on MI355X over the DeepSeek-V3 decode shapes, weights streamed from HBM):
-// one 16-column tile per wave while the activations are a few rows (two once n >= 16384, which
-// leaves >= 512 groups), two at m <= 16, four at m <= 32, and at m <= 64 four when K is long (>= 64
-// blocks) else two, so activation re-reads from L2 stay a fraction of the weight bytes; waves per
-// workgroup sized for ~2048 streaming waves chip-wide (4 or 8, each wave >= 2 K blocks); K split
-// across two workgroups only when that still leaves fewer than 1024 waves, since the split's
-// coherent hand-off costs about a kernel launch. Row tiles 1-2 keep two K blocks in flight per
-// wave; four row tiles keep one (their registers would otherwise spill).
-static Plan8 plan8(int64_t m, int64_t n, int64_t k) {
-  if (m > kSkinnyMaxM) return plan8_lds_best(m, n, k);
+// Skinny plan (m <= 16; measured on MI355X over the DeepSeek-V3 decode shapes, weights streamed from
+// HBM): one 16-column tile per wave while the activations are a few rows (two once n >= 16384, which
+// leaves >= 512 groups), two at m <= 16; waves per workgroup sized for ~2048 streaming waves
+// chip-wide (4 or 8, each wave >= 2 K blocks); K split across two workgroups only when that still
+// leaves fewer than 1024 waves, since the split's coherent hand-off costs about a kernel launch.
+static Plan8 plan8_skinny(int64_t m, int64_t n, int64_t k) {
   Plan8 p;
   p.kind = Kernel8::kSkinny;
   p.tm = p.tn = 0;
   const int64_t KB = k / 128;
   int64_t s = 1;
-  p.mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
-  if (p.mt == 4)
-    p.nt = KB >= 64 ? 4 : 2;
-  else
-    p.nt = m <= 8 ? (n >= 16384 ? 2 : 1) : (m <= 16 ? 2 : 4);
+  p.mt = 1;
+  p.nt = m <= 8 ? (n >= 16384 ? 2 : 1) : 2;
   const int64_t groups = (n + 16 * p.nt - 1) / (16 * p.nt);
   p.grid_x = (int)groups;
-  p.nw = (2048 / groups >= 8 && KB >= 16 && !(p.mt == 4 && p.nt == 4)) ? 8 : 4;
+  p.nw = (2048 / groups >= 8 && KB >= 16) ? 8 : 4;
   if (groups * p.nw < 1024 && KB >= 4 * p.nw) s = 2;
   finish_splits(p, KB, s);
   return p;
+}
+
+// Stream plan (16 < m <= 128; measured on MI355X over the DeepSeek-V3 shapes at m = 32, 64, 128,
+// where it is the fastest or within 4% of the fastest of 1-4 column tiles, 4 or 8 waves, ring depths
+// 2-4, 3-8 A stages and 1-8 K splits): 2, 4 or 8 row tiles, 4 compute waves, two 16-column tiles
+// per wave once n >= 4096 (one below, for more workgroups), and K split in up to 4 parts until about
+// 256 workgroups run (each split >= 4 K blocks).
+static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k) {
+  Plan8 p;
+  p.kind = Kernel8::kStream;
+  p.tm = p.tn = 0;
+  const int64_t KB = k / 128;
+  p.mt = m <= 32 ? 2 : (m <= 64 ? 4 : 8);
+  p.nt = n >= 4096 ? 2 : 1;
+  p.nw = 4;
+  const int64_t groups = (n + 64 * p.nt - 1) / (64 * p.nt);
+  p.grid_x = (int)groups;
+  int64_t s = 256 / groups;
+  if (s > 4) s = 4;
+  if (s > KB / 4) s = KB / 4;
+  finish_splits(p, KB, s);
+  return p;
+}
+
+static Plan8 plan8(int64_t m, int64_t n, int64_t k) {
+  if (m <= kSkinnyMaxM) return plan8_skinny(m, n, k);
+  if (m <= kStreamMaxM) return plan8_stream(m, n, k);
+  return plan8_lds_best(m, n, k);
 }
 
 static size_t workspace8(const Plan8& p, int64_t m, int64_t n) {
@@ -565,33 +865,31 @@ static size_t workspace8(const Plan8& p, int64_t m, int64_t n) {
   return kSplitkCounterBytes + (size_t)p.splits * (size_t)round4(m) * (size_t)n * sizeof(float);
 }
 
-template <int MT, int NT, int NW, int FMT, bool PRE>
+template <int NT, int NW, int FMT, bool PRE>
 static void launch_skinny(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
-  constexpr int D = MT >= 4 ? 1 : 2;
   dim3 grid((unsigned)d.grid_x, (unsigned)d.splits);
-  hipLaunchKernelGGL((gemm8_skinny_kernel<MT, NT, NW, D, FMT, PRE>), grid, dim3(NW * 64), 0, s, a);
-}
-
-template <int MT, int NT, int FMT, bool PRE>
-static void dispatch_skinny_nw(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
-  if (d.nw == 8) launch_skinny<MT, NT, 8, FMT, PRE>(a, d, s);
-  else launch_skinny<MT, NT, 4, FMT, PRE>(a, d, s);
-}
-
-template <int MT, int FMT, bool PRE>
-static void dispatch_skinny_nt(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
-  if (d.nt == 4) dispatch_skinny_nw<MT, 4, FMT, PRE>(a, d, s);
-  else if (d.nt == 2) dispatch_skinny_nw<MT, 2, FMT, PRE>(a, d, s);
-  else dispatch_skinny_nw<MT, 1, FMT, PRE>(a, d, s);
+  hipLaunchKernelGGL((gemm8_skinny_kernel<1, NT, NW, 2, FMT, PRE>), grid, dim3(NW * 64), 0, s, a);
 }
 
 template <int FMT, bool PRE>
 static void dispatch_skinny(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
-  if (d.mt == 1) dispatch_skinny_nt<1, FMT, PRE>(a, d, s);
-  else if (d.mt == 2) dispatch_skinny_nt<2, FMT, PRE>(a, d, s);
-  else if (d.nt == 4) launch_skinny<4, 4, 4, FMT, PRE>(a, d, s);  // 4x4 tiles run with 4 waves only
-  else if (d.nw == 8) launch_skinny<4, 2, 8, FMT, PRE>(a, d, s);
-  else launch_skinny<4, 2, 4, FMT, PRE>(a, d, s);
+  if (d.nt == 2) d.nw == 8 ? launch_skinny<2, 8, FMT, PRE>(a, d, s) : launch_skinny<2, 4, FMT, PRE>(a, d, s);
+  else d.nw == 8 ? launch_skinny<1, 8, FMT, PRE>(a, d, s) : launch_skinny<1, 4, FMT, PRE>(a, d, s);
+}
+
+// Stream kernel: 4 compute waves and 4 A stages; ring depth 2 at 4 row tiles, else 4 (measured).
+template <int MT, int NT, int FMT, bool PRE>
+static void launch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
+  constexpr int D = MT == 4 ? 2 : 4;
+  hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, 4, D, 4, FMT, PRE>), dim3((unsigned)d.grid_x, (unsigned)d.splits),
+                     dim3(5 * 64), 0, s, a);
+}
+
+template <int FMT, bool PRE>
+static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
+  if (d.mt == 2) d.nt == 2 ? launch_stream<2, 2, FMT, PRE>(a, d, s) : launch_stream<2, 1, FMT, PRE>(a, d, s);
+  else if (d.mt == 4) d.nt == 2 ? launch_stream<4, 2, FMT, PRE>(a, d, s) : launch_stream<4, 1, FMT, PRE>(a, d, s);
+  else d.nt == 2 ? launch_stream<8, 2, FMT, PRE>(a, d, s) : launch_stream<8, 1, FMT, PRE>(a, d, s);
 }
 
 // Ring depth per tile shape: as many stages as 160 KiB of LDS holds.
@@ -677,6 +975,9 @@ extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void*
   if (plan.kind == Kernel8::kSkinny) {
     if (e5) pre ? dispatch_skinny<1, true>(g, plan, stream) : dispatch_skinny<1, false>(g, plan, stream);
     else pre ? dispatch_skinny<0, true>(g, plan, stream) : dispatch_skinny<0, false>(g, plan, stream);
+  } else if (plan.kind == Kernel8::kStream) {
+    if (e5) pre ? dispatch_stream<1, true>(g, plan, stream) : dispatch_stream<1, false>(g, plan, stream);
+    else pre ? dispatch_stream<0, true>(g, plan, stream) : dispatch_stream<0, false>(g, plan, stream);
   } else {
     if (e5) pre ? launch_lds<1, true>(g, plan, stream) : launch_lds<1, false>(g, plan, stream);
     else pre ? launch_lds<0, true>(g, plan, stream) : launch_lds<0, false>(g, plan, stream);

@@ -124,12 +124,12 @@ def test_row_major_a_scale_shuffled_b(m):
     _run_and_check(m, 2112, 7168, variant="b_shuffled_row_major_a_scale", seed=11)
 
 
-@pytest.mark.parametrize("m", [7, 300, 777])
+@pytest.mark.parametrize("m", [7, 40, 300, 777])
 def test_mn_scales_bias_fp16(m):
     _run_and_check(m, 2112, 1536, mode="MN", bias=True, out_dtype=torch.float16, seed=21)
 
 
-@pytest.mark.parametrize("m", [16, 256, 640])
+@pytest.mark.parametrize("m", [16, 100, 256, 640])
 def test_e5m2(m):
     _run_and_check(m, 1024, 2048, dtype=torch.float8_e5m2, seed=31)
 
@@ -139,6 +139,17 @@ def test_e5m2(m):
                                    (513, 2112, 256), (600, 144, 384), (1000, 48, 1024)])
 def test_small_and_ragged(m, n, k):
     _run_and_check(m, n, k, seed=41)
+
+
+# Stream-kernel edges (16 < m <= 128): column groups past n (n not a multiple of the group's 64 or 128
+# columns, whole waves past n), one K block, padded row tiles (m = 96 runs 8 row tiles), bias on both
+# store paths (one and two column tiles per wave), and K splits with a ragged last split.
+@pytest.mark.parametrize("m,n,k,bias", [(20, 16, 640, True), (90, 4112, 1024, True), (96, 7168, 2048, False),
+                                        (128, 4096, 128, True), (33, 48, 128, False), (120, 2112, 7168, True),
+                                        (65, 6144, 2304, False)])
+def test_stream_shapes(m, n, k, bias):
+    _run_and_check(m, n, k, bias=bias, seed=51)
+    _run_and_check(m, n, k, variant="b_shuffled", bias=False, seed=52)
 
 
 def test_out_buffer_and_determinism():
