@@ -39,7 +39,7 @@ struct Gemm8Args {
   int m, n, k;
   int out_dtype;
   unsigned* counters;  // one per output tile when splits > 1
-  float* partial;      // when splits > 1: skinny [splits, n, round4(m)], stream and lds [splits, m, n]
+  float* partial;      // when splits > 1: skinny [splits, n, round4(m)], lds [splits, m, n], stream per tile
   int splits;
   int kb_per_split;
 };
@@ -265,17 +265,6 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   const int kb_end = min(KB, kb_begin + p.kb_per_split);
   const int64_t kt32 = p.k >> 5;
 
-  // b_scale of the workgroup's column blocks over its K range (kb_per_split <= 512), staged once.
-  {
-    const int len = kb_end - kb_begin;
-    const int last_row = (p.n - 1) >> 7;
-    for (int i = threadIdx.x; i < kNBlk * len; i += (NW + 1) * 64) {
-      const int r = i / len, kk = i - r * len;
-      sSB[r][kk] = p.sb[(int64_t)min((n0 >> 7) + r, last_row) * p.ldbs + kb_begin + kk];
-    }
-  }
-  __syncthreads();
-
   f32x4 acc[MT][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -283,6 +272,9 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int c0w = n0 + w * NT * 16;  // compute wave's first column
   const int col_w = c0w + 4 * g;     // + nt * 16: the lane's first output column
+  // split-K partials: one plane per split of gridDim.x * NW * MT * NT 1 KiB tiles (fp32 elements)
+  const int64_t stream_plane = (int64_t)gridDim.x * NW * MT * NT * 256;
+  const int64_t part_base = ((int64_t)blockIdx.x * NW + w) * (MT * NT) * 256 + lane * 4;
 
   if (w == NW) {
     // Loader. Rows past m read the out-of-range offset: zeros, no memory access.
@@ -320,6 +312,17 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     // the count exact.
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s) issue(kb_begin + s, s);
+    // b_scale of the workgroup's column blocks over its K range (kb_per_split <= 512), staged once,
+    // behind the first A loads; the first stage barrier publishes it with stage 0.
+    {
+      const int len = kb_end - kb_begin;
+      const int last_row = (p.n - 1) >> 7;
+      for (int i = lane; i < kNBlk * len; i += 64) {
+        const int r = i / len, kk = i - r * len;
+        sSB[r][kk] = p.sb[(int64_t)min((n0 >> 7) + r, last_row) * p.ldbs + kb_begin + kk];
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every load above has landed: the counts below are exact
     int st_fill = NS - 1;
     for (int kb = kb_begin; kb < kb_end; ++kb) {
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * kLoadsA) : "memory");
@@ -397,45 +400,50 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     for (int j = 0; j < D - 1; ++j)
       if (full + j < len) step(kb_begin + full + j, f[j]);
     if (p.splits > 1) {
-      // partials: [split][m][n] fp32; a lane stores its 4 columns of one row as one 16-byte access
-      const rsrc_t prs = partial_rsrc(p.partial, split, (int64_t)p.m * p.n);
+      // partials in accumulator order, [split][group][wave][tile][lane] x 4 fp32: the workgroup that
+      // reduces them runs the same lanes over the same tiles, so every store and load is 1 KiB of
+      // contiguous full lines
+      const rsrc_t prs = partial_rsrc(p.partial, split, stream_plane);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const int row = mt * 16 + li, col = col_w + nt * 16;
-          if (row < p.m && col < p.n) store_partial4(prs, (int64_t)row * p.n + col, acc[mt][nt]);
-        }
+        for (int nt = 0; nt < NT; ++nt) store_partial4(prs, part_base + (mt * NT + nt) * 256, acc[mt][nt]);
     }
   }
 
   if (p.splits > 1) {
     if (!splitk_arrive(p.counters + blockIdx.x, p.splits, &arrive_slot)) return;
     if (w == NW) return;
-    // Sum in split order, each split's MT * NT loads in flight together; positions past m or n read
-    // the out-of-range offset (zeros) and are never stored.
-    const int64_t plane = (int64_t)p.m * p.n;
-    uint32_t poff[MT][NT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int row = mt * 16 + li, col = col_w + nt * 16;
-        poff[mt][nt] = row < p.m && col < p.n ? (uint32_t)(((int64_t)row * p.n + col) * 4) : kOobOffset;
-        acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Each coherent load is a trip to the memory side, so loads go in rounds of up to 32 per lane
+    // (the weight ring and fragment registers are free by now): chunks of up to 8 tiles times batches
+    // of 4 splits, slots past the last split loading zeros. Per tile the sum runs in split order.
+    constexpr int T = MT * NT, kBatch = 4, kChunk = T < 8 ? T : 8;
+    for (int sp0 = 0; sp0 < p.splits; sp0 += kBatch) {
+      rsrc_t r[kBatch];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b)
+        r[b] = partial_rsrc(p.partial, sp0 + b < p.splits ? sp0 + b : 0, stream_plane);
+#pragma unroll
+      for (int t0 = 0; t0 < T; t0 += kChunk) {
+        f32x4 v[kChunk][kBatch];
+#pragma unroll
+        for (int c = 0; c < kChunk; ++c)
+#pragma unroll
+          for (int b = 0; b < kBatch; ++b)
+            v[c][b] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           r[b], sp0 + b < p.splits ? (int)((part_base + (t0 + c) * 256) * 4) : (int)kOobOffset, 0,
+                           kSc1));
+#pragma unroll
+        for (int c = 0; c < kChunk; ++c)
+#pragma unroll
+          for (int b = 0; b < kBatch; ++b) acc[(t0 + c) / NT][(t0 + c) % NT] += v[c][b];
+        __builtin_amdgcn_sched_barrier(0);  // one round at a time
       }
-    for (int sp = 0; sp < p.splits; ++sp) {
-      const rsrc_t r = partial_rsrc(p.partial, sp, plane);
-      f32x4 v[MT][NT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          v[mt][nt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)poff[mt][nt], 0, kSc1));
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] += v[mt][nt];
     }
   }
   if (w == NW) return;
@@ -862,6 +870,8 @@ static Plan8 plan8(int64_t m, int64_t n, int64_t k) {
 
 static size_t workspace8(const Plan8& p, int64_t m, int64_t n) {
   if (p.splits <= 1) return 0;
+  if (p.kind == Kernel8::kStream)  // whole 16x16 tiles of every wave of every column group
+    return kSplitkCounterBytes + (size_t)p.splits * (size_t)p.grid_x * p.nw * p.mt * p.nt * 1024;
   return kSplitkCounterBytes + (size_t)p.splits * (size_t)round4(m) * (size_t)n * sizeof(float);
 }
 
