@@ -39,7 +39,7 @@ struct Gemm8Args {
   int m, n, k;
   int out_dtype;
   unsigned* counters;  // one per output tile when splits > 1
-  float* partial;      // when splits > 1: skinny [splits, n, round4(m)], lds [splits, m, n], stream per tile
+  float* partial;      // when splits > 1: skinny [splits, n, round4(m)]; stream and lds per 16x16 tile
   int splits;
   int kb_per_split;
 };
@@ -666,26 +666,24 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   const int row_w = m0 + wm * (TM / 2) + li;  // + mt * 16: the lane's output row
   const int col_w = n0 + wn * (TN / 4) + 4 * g;  // + nt * 16: the lane's first output column
   if (p.splits > 1) {
-    // partials: [split][m][n] fp32; a lane stores its 4 columns of one row as one 16-byte access
-    const int64_t plane = (int64_t)p.m * p.n;
+    // partials in accumulator order, [split][tile][wave][mt][nt][lane] x 4 fp32: the workgroup that
+    // reduces them runs the same lanes over the same tiles, so every store and load is 1 KiB of
+    // contiguous full lines
+    const int64_t plane = (int64_t)tiles_m * tiles_n * TM * TN;
+    const int64_t part_base = ((int64_t)pid * 8 + w) * (MT * NT) * 256 + lane * 4;
     const rsrc_t prs = partial_rsrc(p.partial, split, plane);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int row = row_w + mt * 16, col = col_w + nt * 16;
-        if (row < p.m && col < p.n) store_partial4(prs, (int64_t)row * p.n + col, acc[mt][nt]);
-      }
+      for (int nt = 0; nt < NT; ++nt) store_partial4(prs, part_base + (mt * NT + nt) * 256, acc[mt][nt]);
     if (!splitk_arrive(p.counters + pid, p.splits, &arrive_slot)) return;
-    // Sum in split order, one split at a time, with all MT * NT loads of a split in flight together.
-    // Out-of-range positions read the out-of-range offset (zeros) and are never stored.
+    // Sum in split order, with all MT * NT loads of a batch of splits in flight together.
     uint32_t poff[MT][NT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const int row = row_w + mt * 16, col = col_w + nt * 16;
-        poff[mt][nt] = row < p.m && col < p.n ? (uint32_t)(((int64_t)row * p.n + col) * 4) : kOobOffset;
+        poff[mt][nt] = (uint32_t)((part_base + (mt * NT + nt) * 256) * 4);
         acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
     // Splits go in batches of up to kBatch whose loads are all issued before any is added (each
@@ -872,6 +870,8 @@ static size_t workspace8(const Plan8& p, int64_t m, int64_t n) {
   if (p.splits <= 1) return 0;
   if (p.kind == Kernel8::kStream)  // whole 16x16 tiles of every wave of every column group
     return kSplitkCounterBytes + (size_t)p.splits * (size_t)p.grid_x * p.nw * p.mt * p.nt * 1024;
+  if (p.kind == Kernel8::kLds)  // whole workgroup tiles
+    return kSplitkCounterBytes + (size_t)p.splits * (size_t)p.grid_x * p.tm * p.tn * sizeof(float);
   return kSplitkCounterBytes + (size_t)p.splits * (size_t)round4(m) * (size_t)n * sizeof(float);
 }
 
@@ -887,10 +887,10 @@ static void dispatch_skinny(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   else d.nw == 8 ? launch_skinny<1, 8, FMT, PRE>(a, d, s) : launch_skinny<1, 4, FMT, PRE>(a, d, s);
 }
 
-// Stream kernel: 4 compute waves and 4 A stages; ring depth 2 at 4 row tiles, else 4 (measured).
+// Stream kernel: 4 compute waves and 4 A stages; ring depth 4 at 2 row tiles, else 2 (measured).
 template <int MT, int NT, int FMT, bool PRE>
 static void launch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
-  constexpr int D = MT == 4 ? 2 : 4;
+  constexpr int D = MT == 2 ? 4 : 2;
   hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, 4, D, 4, FMT, PRE>), dim3((unsigned)d.grid_x, (unsigned)d.splits),
                      dim3(5 * 64), 0, s, a);
 }
