@@ -546,15 +546,16 @@ __global__ __launch_bounds__(512) void gemm4_lds_kernel(Gemm4Args p) {
   const int row_w = m0 + wm * (TM / 2) + li;
   const int col_w = n0 + wn * (TN / 4) + 4 * g;
   if (p.splits > 1) {
-    const int64_t plane = (int64_t)p.m * p.n;
+    // partials in accumulator order, [split][tile][wave][mt][nt][lane] x 4 fp32: the workgroup that
+    // reduces them runs the same lanes over the same tiles, so every store and load is 1 KiB of
+    // contiguous full lines
+    const int64_t plane = (int64_t)tiles_m * tiles_n * TM * TN;
+    const int64_t part_base = ((int64_t)pid * 8 + w) * (MT * NT) * 256 + lane * 4;
     const rsrc_t prs = partial_rsrc(p.partial, split, plane);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int row = row_w + mt * 16, col = col_w + nt * 16;
-        if (row < p.m && col < p.n) store_partial4(prs, (int64_t)row * p.n + col, acc[mt][nt]);
-      }
+      for (int nt = 0; nt < NT; ++nt) store_partial4(prs, part_base + (mt * NT + nt) * 256, acc[mt][nt]);
     if (!splitk_arrive(p.counters + pid, p.splits, &arrive_slot)) return;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -565,11 +566,9 @@ __global__ __launch_bounds__(512) void gemm4_lds_kernel(Gemm4Args p) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const int row = row_w + mt * 16, col = col_w + nt * 16;
-          const uint32_t off = row < p.m && col < p.n ? (uint32_t)(((int64_t)row * p.n + col) * 4) : kOobOffset;
-          acc[mt][nt] += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kSc1));
-        }
+        for (int nt = 0; nt < NT; ++nt)
+          acc[mt][nt] += __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)((part_base + (mt * NT + nt) * 256) * 4), 0, kSc1));
     }
   }
 
@@ -709,17 +708,22 @@ static void launch_lds4(const Gemm4Args& g, const Lds4Plan& p, hipStream_t s) {
 
 using namespace aklr;
 
-// Workspace: kSplitkCounterBytes of arrival counters (the LDS kernel's split-K), then fp32 partials
-// [splits, m, n]. The LDS kernel may be declined at call time (row-major scales with unaligned rows),
-// so the size covers whichever path could run.
+// Workspace: kSplitkCounterBytes of arrival counters, then fp32 partials: [splits, n, round4(m)] for
+// the skinny kernel, whole workgroup tiles for the LDS kernel. The LDS kernel may be declined at call
+// time (row-major scales with unaligned rows); the tile kernel that runs instead does not split K.
+static size_t lds4_partial_bytes(const Lds4Plan& p) {
+  return (size_t)p.splits * (size_t)p.tiles * p.tm * p.tn * sizeof(float);
+}
+
 extern "C" size_t aklr_gemm_a4w4_mxfp4_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k < 64) return 0;
-  int splits = 1;
-  if (m <= kDecode4MaxM)
-    splits = plan_skinny4(m, n, k).splits;
-  else if (k % 256 == 0)
-    splits = plan_lds4(m, n, k).splits;
-  return splits > 1 ? kSplitkCounterBytes + (size_t)splits * (size_t)round4(m) * (size_t)n * sizeof(float) : 0;
+  if (m <= kDecode4MaxM) {
+    const Skinny4Plan d = plan_skinny4(m, n, k);
+    return d.splits > 1 ? kSplitkCounterBytes + (size_t)d.splits * (size_t)round4(m) * (size_t)n * sizeof(float) : 0;
+  }
+  if (k % 256 != 0) return 0;
+  const Lds4Plan lp = plan_lds4(m, n, k);
+  return lp.splits > 1 ? kSplitkCounterBytes + lds4_partial_bytes(lp) : 0;
 }
 
 extern "C" int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb,
@@ -787,7 +791,7 @@ extern "C" int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t
     g.splits = lp.splits;
     g.ks_per_split = lp.ks_per_split;
     if (lp.splits > 1) {
-      const size_t need = kSplitkCounterBytes + (size_t)lp.splits * (size_t)m * (size_t)n * sizeof(float);
+      const size_t need = kSplitkCounterBytes + lds4_partial_bytes(lp);
       if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) return AKLR_ERR_WORKSPACE;
       g.counters = static_cast<unsigned*>(workspace);
       g.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kSplitkCounterBytes);
