@@ -5,13 +5,10 @@
 // with one FMA per element: acc += partial * (a_scale[row, kb] * b_scale[n/128, kb]). The fp32 block
 // scales are not powers of two, so they cannot ride the MFMA's e8m0 scale operands.
 //
-// * skinny (m <= 16): weight streaming. A workgroup owns 16*NT output columns and a K range; each of
-//   its waves streams its own contiguous K sub-range of the weight straight from HBM into MFMA
-//   operand registers (no LDS), D K-blocks in flight, with the activations from L2. The waves'
-//   accumulators are summed in one LDS tile in wave order.
-// * stream (16 < m <= 128): weight streaming with the activations shared through LDS. Each compute
-//   wave streams its own weight columns over the workgroup's K range into a register ring, and a
-//   loader wave fills an LDS ring with each K block of A in MFMA fragment order.
+// * stream (m <= 128): weight streaming with the activations shared through LDS. Each compute wave
+//   streams its own weight columns over the workgroup's K range from HBM straight into MFMA operand
+//   registers (a register ring, no LDS), and a loader wave fills an LDS ring with each K block of A
+//   in MFMA fragment order.
 // * lds (m > 128): 256x256, 256x128, 128x256 or 128x128 workgroup tiles of 8 waves, K steps of 128
 //   through a 2- to 4-stage LDS ring filled by direct-to-LDS loads (16-byte chunks XOR-swizzled by
 //   row), a_scale staged in LDS, XCD-aware tile order, 16-byte output stores.
@@ -39,188 +36,18 @@ struct Gemm8Args {
   int m, n, k;
   int out_dtype;
   unsigned* counters;  // one per output tile when splits > 1
-  float* partial;      // when splits > 1: skinny [splits, n, round4(m)]; stream and lds per 16x16 tile
+  float* partial;      // when splits > 1: per 16x16 tile, in accumulator order
   int splits;
   int kb_per_split;
 };
 
-// Offset, in a PRESHUFFLE_16x16 weight with kt32 = k/32 column tiles, of the 16 bytes that MFMA lane
-// group g (0..3) needs for row `col` and K block kb: k = 16g.. (tile 4kb + g/2, half g%2) and
-// k = 64+16g.. (tile 4kb + 2 + g/2). Returns the first; the second is +1024. The 64 lanes of one
-// load read 1 KiB: two runs of 512 contiguous bytes.
-__device__ __forceinline__ int64_t preshuffle_frag_offset(int64_t col, int64_t kt32, int kb, int g) {
-  return ((col >> 4) * kt32 + (int64_t)kb * 4 + (g >> 1)) * 512 + (g & 1) * 256 + (col & 15) * 16;
-}
-
-// ---------------------------------------------------------------------------------------------
-// skinny
-template <int MT, int NT>
-struct SkinnyFrag {
-  i32x8 a[MT];
-  i32x8 b[NT];
-  float sa[MT][4];
-  float sb[NT];
-};
-
-template <int MT, int NT, int NW, int D, int FMT, bool PRE>
-__global__ __launch_bounds__(NW * 64) void gemm8_skinny_kernel(Gemm8Args p) {
-  constexpr int T = MT * NT;
-  __shared__ f32x4 red[T][64];
-  __shared__ unsigned arrive_slot;
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: K ranges live in SGPRs
-  const int li = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 16 * NT;
-  const int split = blockIdx.y;
-  const int KB = p.k >> 7;
-  const int kb_base = split * p.kb_per_split;
-  const int kb_len = min(p.kb_per_split, KB - kb_base);
-  const int chunk = (kb_len + NW - 1) / NW;
-  const int kb_begin = kb_base + min(w * chunk, kb_len);
-  const int kb_end = kb_base + min((w + 1) * chunk, kb_len);
-  const int64_t kt32 = p.k >> 5;
-
-  // A and B come through raw buffer loads whose per-block offset is switched off (kOobOffset: zeros,
-  // no memory access) past the wave's K range, so the loop below refills its register ring with no
-  // branch. Rows past m and column tiles past n read row/tile 0 instead: they only feed output rows
-  // and columns that are never stored. B gets one descriptor per 16-column tile (offsets < 16*ldb).
-  rsrc_t brs[NT];
-  const float* sbp[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int64_t c0 = (n0 + nt * 16) < p.n ? n0 + nt * 16 : 0;  // n % 16 == 0: validity per tile
-    if (PRE)
-      brs[nt] = make_rsrc(p.b + (c0 >> 4) * kt32 * 512, (uint32_t)(kt32 * 512));
-    else
-      brs[nt] = make_rsrc(p.b + c0 * p.ldb, (uint32_t)(15 * p.ldb + p.k));
-    sbp[nt] = p.sb + (c0 >> 7) * p.ldbs;
-  }
-  const uint32_t b_lane = PRE ? (uint32_t)((g >> 1) * 512 + (g & 1) * 256 + li * 16)
-                              : (uint32_t)(li * p.ldb + g * 16);
-  // Activation fragments and a_scale are loaded only by lanes whose rows exist: the others get the
-  // out-of-range offset (zeros, no request), which for m < 16 removes most of their L2 traffic.
-  const rsrc_t ars = make_rsrc(p.a, (uint32_t)((p.m - 1) * p.lda + p.k));
-  const rsrc_t sars = make_rsrc(p.sa, (uint32_t)(((p.m - 1) * p.sa_sm + (KB - 1) * p.sa_sk + 1) * 4));
-  uint32_t a_lane[MT];
-  uint32_t sa_lane[MT][4];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int row = mt * 16 + li;
-    a_lane[mt] = row < p.m ? (uint32_t)(row * p.lda + g * 16) : kOobOffset;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int srow = mt * 16 + 4 * g + r;
-      sa_lane[mt][r] = srow < p.m ? (uint32_t)(srow * p.sa_sm * 4) : kOobOffset;
-    }
-  }
-  const uint32_t sa_kstep = (uint32_t)(p.sa_sk * 4);
-
-  auto load = [&](int kb, SkinnyFrag<MT, NT>& f) {
-    const bool on = kb < kb_end;
-    const int kbc = min(kb, KB - 1);  // b_scale: any valid block (its product with zero data is 0)
-    const uint32_t boff = on ? (uint32_t)(PRE ? kb * 2048 : kb * 128) : kOobOffset;
-    const uint32_t aoff = on ? (uint32_t)(kb * 128) : kOobOffset;
-    const uint32_t soff = on ? (uint32_t)kb * sa_kstep : kOobOffset;
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      f.b[nt] = cat(buf_ld16<kNt>(brs[nt], b_lane + boff), buf_ld16<kNt>(brs[nt], b_lane + boff + (PRE ? 1024 : 64)));
-      f.sb[nt] = sbp[nt][kbc];
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      f.a[mt] = cat(buf_ld16(ars, a_lane[mt] + aoff), buf_ld16(ars, a_lane[mt] + aoff + 64));
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        f.sa[mt][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sars, (int)(sa_lane[mt][r] + soff), 0, 0));
-    }
-  };
-
-  f32x4 acc[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // D-deep register ring: block kb0 + j lives in f[j]; once consumed, the slot is refilled with block
-  // kb0 + j + D. Blocks past kb_end load as zeros, so the last group needs no special case.
-  SkinnyFrag<MT, NT> f[D];
-#pragma unroll
-  for (int j = 0; j < D; ++j) load(kb_begin + j, f[j]);
-  for (int kb0 = kb_begin; kb0 < kb_end; kb0 += D) {
-#pragma unroll
-    for (int j = 0; j < D; ++j) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-          const f32x4 part = mfma16x128<FMT>(f[j].a[mt], f[j].b[nt], z);
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            acc[mt][nt][r] = fmaf(part[r], f[j].sa[mt][r] * f[j].sb[nt], acc[mt][nt][r]);
-        }
-      load(kb0 + j + D, f[j]);
-      __builtin_amdgcn_sched_barrier(0);  // refill slot j before consuming slot j + 1
-    }
-  }
-
-  // Sum the waves' accumulators in wave order: wave 0 stores, waves 1.. NW-1 add in turn.
-  for (int v = 0; v < NW; ++v) {
-    if (w == v) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const int t = mt * NT + nt;
-          red[t][lane] = v == 0 ? acc[mt][nt] : red[t][lane] + acc[mt][nt];
-        }
-    }
-    __syncthreads();
-  }
-
-  // Wave w owns tiles t = w, w + NW, ...: it writes the output (one split) or its fp32 partial.
-  const int64_t m4 = round4(p.m);
-  const int64_t plane = (int64_t)p.n * m4;
-  for (int t = w; t < T; t += NW) {
-    const int mt = t / NT, nt = t % NT;
-    const int c0 = n0 + nt * 16;
-    if (c0 >= p.n) continue;
-    const f32x4 s = red[t][lane];
-    const int col = c0 + li;
-    const int row0 = mt * 16 + 4 * g;
-    if (p.splits > 1) {
-      if (row0 < p.m) store_partial4(partial_rsrc(p.partial, split, plane), (int64_t)col * m4 + row0, s);
-      continue;
-    }
-    const float bv = p.bias ? p.bias[col] : 0.0f;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (row0 + r < p.m) store_out(p.out, (int64_t)(row0 + r) * p.ldo + col, s[r] + bv, p.out_dtype);
-  }
-  if (p.splits == 1) return;
-  if (!splitk_arrive(p.counters + blockIdx.x, p.splits, &arrive_slot)) return;
-  for (int t = w; t < T; t += NW) {
-    const int mt = t / NT, nt = t % NT;
-    const int c0 = n0 + nt * 16;
-    const int row0 = mt * 16 + 4 * g;
-    if (c0 >= p.n || row0 >= p.m) continue;
-    const int col = c0 + li;
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < p.splits; ++sp) v += load_partial4(partial_rsrc(p.partial, sp, plane), (int64_t)col * m4 + row0);
-    const float bv = p.bias ? p.bias[col] : 0.0f;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (row0 + r < p.m) store_out(p.out, (int64_t)(row0 + r) * p.ldo + col, v[r] + bv, p.out_dtype);
-  }
-}
-
 // ---------------------------------------------------------------------------------------------
 // stream: weight streaming with the activations shared through LDS, for a few row tiles (MT <= 8).
 // A workgroup owns NW * NT * 16 output columns and a K range. Its NW compute waves own NT 16-column
-// tiles each and stream those weight columns from HBM straight into a D-deep register ring, as the
-// skinny kernel does; one more wave, the loader, moves each 128-wide K block of A (all MT row tiles)
-// and its a_scale column into an NS-stage LDS ring with direct-to-LDS loads, so A crosses L2 once per
-// workgroup instead of once per wave. A lands in MFMA fragment order -- 1 KiB chunk (mt, h) holds at
+// tiles each and stream those weight columns from HBM straight into a D-deep register ring (loads
+// past the K range use an out-of-range offset: zeros, no memory access); one more wave, the loader,
+// moves each 128-wide K block of A (all MT row tiles) and its a_scale column into an NS-stage LDS ring
+// with direct-to-LDS loads, so A crosses L2 once per workgroup instead of once per wave. A lands in MFMA fragment order -- 1 KiB chunk (mt, h) holds at
 // lane l's 16 bytes row mt * 16 + l % 16, bytes 64h + 16 (l / 16) of the block -- and every compute
 // read is one contiguous ds_read_b128.
 // The loader issues only LDS-bound loads and the compute waves only register-bound ones, so both
@@ -744,18 +571,17 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
 // ---------------------------------------------------------------------------------------------
 // host-side planning
 
-// m <= kSkinnyMaxM streams the weight through the skinny kernel, m <= kStreamMaxM through the stream
-// kernel (activations shared in LDS); larger m runs the LDS kernel.
-static constexpr int64_t kSkinnyMaxM = 16;
+// m <= kStreamMaxM streams the weight through the stream kernel (activations shared in LDS); larger m
+// runs the LDS kernel.
 static constexpr int64_t kStreamMaxM = 128;
 
-enum class Kernel8 { kSkinny, kStream, kLds };
+enum class Kernel8 { kStream, kLds };
 
 struct Plan8 {
   Kernel8 kind;
-  int mt, nt, nw;    // skinny, stream: 16-row and 16-column tiles per wave, waves per workgroup
+  int mt, nt, nw;    // stream: 16-row and 16-column tiles per wave, compute waves per workgroup
   int tm, tn;        // lds: workgroup tile
-  int grid_x;        // skinny, stream: column groups; lds: output tiles
+  int grid_x;        // stream: column groups; lds: output tiles
   int splits, kb_per_split;
 };
 
@@ -817,30 +643,9 @@ static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
   return best;
 }
 
-// Skinny plan (m <= 16; measured on MI355X over the DeepSeek-V3 decode shapes, weights streamed from
-// HBM): one 16-column tile per wave while the activations are a few rows (two once n >= 16384, which
-// leaves >= 512 groups), two at m <= 16; waves per workgroup sized for ~2048 streaming waves
-// chip-wide (4 or 8, each wave >= 2 K blocks); K split across two workgroups only when that still
-// leaves fewer than 1024 waves, since the split's coherent hand-off costs about a kernel launch.
-static Plan8 plan8_skinny(int64_t m, int64_t n, int64_t k) {
-  Plan8 p;
-  p.kind = Kernel8::kSkinny;
-  p.tm = p.tn = 0;
-  const int64_t KB = k / 128;
-  int64_t s = 1;
-  p.mt = 1;
-  p.nt = m <= 8 ? (n >= 16384 ? 2 : 1) : 2;
-  const int64_t groups = (n + 16 * p.nt - 1) / (16 * p.nt);
-  p.grid_x = (int)groups;
-  p.nw = (2048 / groups >= 8 && KB >= 16) ? 8 : 4;
-  if (groups * p.nw < 1024 && KB >= 4 * p.nw) s = 2;
-  finish_splits(p, KB, s);
-  return p;
-}
-
-// Stream plan (16 < m <= 128; measured on MI355X over the DeepSeek-V3 shapes at m = 32, 64, 128,
+// Stream plan (m <= 128; measured on MI355X over the DeepSeek-V3 shapes at m = 1, 16, 32, 64, 128,
 // where it is the fastest or within 4% of the fastest of 1-4 column tiles, 4 or 8 waves, ring depths
-// 2-4, 3-8 A stages and 1-8 K splits): 2, 4 or 8 row tiles, 4 compute waves, two 16-column tiles
+// 2-4, 3-8 A stages and 1-8 K splits): 1, 2, 4 or 8 row tiles, 4 compute waves, two 16-column tiles
 // per wave once n >= 4096 (one below, for more workgroups), and K split in up to 4 parts until about
 // 256 workgroups run (each split >= 4 K blocks).
 static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k) {
@@ -848,7 +653,7 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k) {
   p.kind = Kernel8::kStream;
   p.tm = p.tn = 0;
   const int64_t KB = k / 128;
-  p.mt = m <= 32 ? 2 : (m <= 64 ? 4 : 8);
+  p.mt = m <= 16 ? 1 : (m <= 32 ? 2 : (m <= 64 ? 4 : 8));
   p.nt = n >= 4096 ? 2 : 1;
   p.nw = 4;
   const int64_t groups = (n + 64 * p.nt - 1) / (64 * p.nt);
@@ -861,43 +666,30 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k) {
 }
 
 static Plan8 plan8(int64_t m, int64_t n, int64_t k) {
-  if (m <= kSkinnyMaxM) return plan8_skinny(m, n, k);
   if (m <= kStreamMaxM) return plan8_stream(m, n, k);
   return plan8_lds_best(m, n, k);
 }
 
-static size_t workspace8(const Plan8& p, int64_t m, int64_t n) {
+static size_t workspace8(const Plan8& p) {
   if (p.splits <= 1) return 0;
   if (p.kind == Kernel8::kStream)  // whole 16x16 tiles of every wave of every column group
     return kSplitkCounterBytes + (size_t)p.splits * (size_t)p.grid_x * p.nw * p.mt * p.nt * 1024;
-  if (p.kind == Kernel8::kLds)  // whole workgroup tiles
-    return kSplitkCounterBytes + (size_t)p.splits * (size_t)p.grid_x * p.tm * p.tn * sizeof(float);
-  return kSplitkCounterBytes + (size_t)p.splits * (size_t)round4(m) * (size_t)n * sizeof(float);
+  // lds: whole workgroup tiles
+  return kSplitkCounterBytes + (size_t)p.splits * (size_t)p.grid_x * p.tm * p.tn * sizeof(float);
 }
 
-template <int NT, int NW, int FMT, bool PRE>
-static void launch_skinny(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
-  dim3 grid((unsigned)d.grid_x, (unsigned)d.splits);
-  hipLaunchKernelGGL((gemm8_skinny_kernel<1, NT, NW, 2, FMT, PRE>), grid, dim3(NW * 64), 0, s, a);
-}
-
-template <int FMT, bool PRE>
-static void dispatch_skinny(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
-  if (d.nt == 2) d.nw == 8 ? launch_skinny<2, 8, FMT, PRE>(a, d, s) : launch_skinny<2, 4, FMT, PRE>(a, d, s);
-  else d.nw == 8 ? launch_skinny<1, 8, FMT, PRE>(a, d, s) : launch_skinny<1, 4, FMT, PRE>(a, d, s);
-}
-
-// Stream kernel: 4 compute waves and 4 A stages; ring depth 4 at 2 row tiles, else 2 (measured).
+// Stream kernel: 4 compute waves and 4 A stages; ring depth 4 at 1-2 row tiles, else 2 (measured).
 template <int MT, int NT, int FMT, bool PRE>
 static void launch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
-  constexpr int D = MT == 2 ? 4 : 2;
+  constexpr int D = MT <= 2 ? 4 : 2;
   hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, 4, D, 4, FMT, PRE>), dim3((unsigned)d.grid_x, (unsigned)d.splits),
                      dim3(5 * 64), 0, s, a);
 }
 
 template <int FMT, bool PRE>
 static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
-  if (d.mt == 2) d.nt == 2 ? launch_stream<2, 2, FMT, PRE>(a, d, s) : launch_stream<2, 1, FMT, PRE>(a, d, s);
+  if (d.mt == 1) d.nt == 2 ? launch_stream<1, 2, FMT, PRE>(a, d, s) : launch_stream<1, 1, FMT, PRE>(a, d, s);
+  else if (d.mt == 2) d.nt == 2 ? launch_stream<2, 2, FMT, PRE>(a, d, s) : launch_stream<2, 1, FMT, PRE>(a, d, s);
   else if (d.mt == 4) d.nt == 2 ? launch_stream<4, 2, FMT, PRE>(a, d, s) : launch_stream<4, 1, FMT, PRE>(a, d, s);
   else d.nt == 2 ? launch_stream<8, 2, FMT, PRE>(a, d, s) : launch_stream<8, 1, FMT, PRE>(a, d, s);
 }
@@ -924,7 +716,7 @@ using namespace aklr;
 
 extern "C" size_t aklr_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k < 128) return 0;
-  return workspace8(plan8(m, n, k), m, n);
+  return workspace8(plan8(m, n, k));
 }
 
 extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void* b, int64_t ldb,
@@ -977,15 +769,12 @@ extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void*
   g.splits = plan.splits;
   g.kb_per_split = plan.kb_per_split;
   if (plan.splits > 1) {
-    const size_t need = workspace8(plan, m, n);
+    const size_t need = workspace8(plan);
     if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) return AKLR_ERR_WORKSPACE;
     g.counters = static_cast<unsigned*>(workspace);
     g.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kSplitkCounterBytes);
   }
-  if (plan.kind == Kernel8::kSkinny) {
-    if (e5) pre ? dispatch_skinny<1, true>(g, plan, stream) : dispatch_skinny<1, false>(g, plan, stream);
-    else pre ? dispatch_skinny<0, true>(g, plan, stream) : dispatch_skinny<0, false>(g, plan, stream);
-  } else if (plan.kind == Kernel8::kStream) {
+  if (plan.kind == Kernel8::kStream) {
     if (e5) pre ? dispatch_stream<1, true>(g, plan, stream) : dispatch_stream<1, false>(g, plan, stream);
     else pre ? dispatch_stream<0, true>(g, plan, stream) : dispatch_stream<0, false>(g, plan, stream);
   } else {

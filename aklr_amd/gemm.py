@@ -185,7 +185,7 @@ def gemm_a8w8_blockwise_scaled(
     if not workspace.ready(a.device, _lib.lib().aklr_gemm_a8w8_blockscale_workspace_bytes(m, n, k)):
         return FallbackReason.NOT_WARMED
     b_layout = _lib.B_ROW_MAJOR if variant == "row_major" else _lib.B_PRESHUFFLE_16x16
-    path = "skinny" if m <= 16 else ("stream" if m <= 128 else "lds")  # the library picks the same way
+    path = "stream" if m <= 128 else "lds"  # the library picks the same way (kStreamMaxM)
     return _Gemm8Plan(a, b, a_scale, b_scale, bias, out, dt, m, n, k, sa_sm, sa_sk, b_layout, variant,
                       f"aklr_gemm_a8w8_blockscale:{path}")
 

@@ -10,7 +10,7 @@ Each step is one HIP graph; steps rotate over enough weight copies (> 512 MB per
 
 value = whole-step algorithmic bytes / step time, in GB/s (bytes per GEMM: M*K + 4*M*K/128 + N*K +
 4*ceil(N/128)*K/128 + 2*M*N; per quant: 3.03125*M*K).
-roofline: the dominant kernel, the skinny (decode) GEMM at M=16, (N, K) = (7168, 16384) (117.97 MB per
+roofline: the dominant kernel, the stream (decode) GEMM at M=16, (N, K) = (7168, 16384) (117.97 MB per
 launch), timed alone with HIP events on its stream over graph replays; peak 8 TB/s.
 roofline.traffic: HBM bytes per launch of that kernel from two rocprofv3 --pmc runs (FETCH_SIZE, then
 WRITE_SIZE) of ``python3 bench.py --probe-traffic``, each scaled by what the counter reads for a plain
@@ -232,7 +232,7 @@ def moe_figures(dev, steps=10):
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                            "gemm8_skinny_m16_n7168_k16384_traffic.json")
+                            "gemm8_stream_m16_n7168_k16384_traffic.json")
 
 
 def probe_traffic(dev, stream):
@@ -392,7 +392,7 @@ def main(argv=None):
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"gemm8_skinny_kernel (M={m_dom}, N={n_dom}, K={k_dom})",
+            "kernel": f"gemm8_stream_kernel (M={m_dom}, N={n_dom}, K={k_dom})",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

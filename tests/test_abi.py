@@ -71,7 +71,10 @@ def test_invalid_arguments_rejected_before_launch(native_lib):
 def test_workspace_sizes_are_host_computable(native_lib):
     L = native_lib
     assert L.aklr_gemm_a8w8_blockscale_workspace_bytes(0, 16, 128) == 0
-    for m, n, k in ((1, 2112, 7168), (16, 7168, 16384), (4096, 7168, 16384), (128, 24576, 1536)):
+    up = lambda x, q: -(-x // q) * q
+    for m, n, k in ((1, 2112, 7168), (16, 7168, 16384), (4096, 7168, 16384), (128, 24576, 1536), (256, 2112, 7168)):
         ws = L.aklr_gemm_a8w8_blockscale_workspace_bytes(m, n, k)
-        assert ws % 4 == 0 and ws <= 64 * m * n * 4
+        # 64 KiB of split-K counters plus at most 8 splits of fp32 partials over whole 16x16 tiles of
+        # workgroups at most 256 x 256
+        assert ws % 1024 == 0 and ws <= 65536 + 8 * up(m, 256) * up(n, 256) * 4
     assert L.aklr_gemm_a4w4_mxfp4_workspace_bytes(1, 10240, 8192) % 4 == 0

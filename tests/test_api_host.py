@@ -76,7 +76,7 @@ def _g8(m=4, n=144, k=256, **kw):
 def test_gemm8_variants(as_gpu):
     a, b, sa, sb = _g8()
     s = aklr_amd.gemm_a8w8_blockwise_scaled.serving(a, b, sa, sb)
-    assert s.variant == "row_major" and s.kernel_ref.endswith(":skinny")
+    assert s.variant == "row_major" and s.kernel_ref.endswith(":stream")
     assert aklr_amd.gemm_a8w8_blockwise_scaled.serving(fp8((300, 256)), b, torch.ones((300, 2)), sb).kernel_ref.endswith(":lds")
     # MN-major a_scale
     assert not isinstance(aklr_amd.gemm_a8w8_blockwise_scaled.serving(a, b, sa.t().contiguous(), sb,
