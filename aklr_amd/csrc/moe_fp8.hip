@@ -233,13 +233,14 @@ __device__ __forceinline__ int class_blocks(int c, int k) {
 
 __global__ __launch_bounds__(1024) void align_kernel(const int32_t* __restrict__ ids, int R, int S, int E,
                                                      int32_t* __restrict__ row_of, int32_t* __restrict__ sorted_tok,
-                                                     BlockTable bt) {
+                                                     BlockTable bt, int* __restrict__ tickets) {
   __shared__ int cnt[kMaxExperts];
   __shared__ int off[kMaxExperts];
   __shared__ int boff[kClasses][kMaxExperts];
   __shared__ int wsum[16];
   __shared__ int total;
   const int tid = threadIdx.x;
+  if (tid < 2) tickets[tid] = 0;  // the grouped GEMMs' work-item counters (gate-up, down)
   for (int e = tid; e < kMaxExperts; e += 1024) cnt[e] = 0;
   __syncthreads();
   for (int i = tid; i < R; i += 1024) {
@@ -335,10 +336,12 @@ struct MoeGemmArgs {
   int64_t b_stride;          // bytes per expert
   const float* sb;           // [experts, ceil(N/128), K/128]
   int64_t sb_stride;         // floats per expert
-  const int32_t* blk_expert;
+  const int32_t* blk_expert;  // block table of class 0; class k at + k * blk_cap
   const int32_t* blk_row;
   const int32_t* blk_rows;
-  const int32_t* nblk;
+  const int32_t* nblk;        // blocks per class
+  int blk_cap;
+  int* tickets;               // work-item counter, zero at launch (align_kernel clears it)
   int K, N, I;               // reduction length, weight rows, intermediate size
   int tiles_n;               // GATEUP: I / 128; DOWN: ceil(N / 256)
   uint8_t* hq;               // GATEUP out: [R, I] codes
@@ -351,26 +354,40 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
 __device__ __forceinline__ float round_bf16(float v) { return __uint_as_float(f32_to_bf16_bits(v) << 16); }
 
-// TM-row blocks (one class of the block table) x 256 weight rows; 8 waves in 2 (m) x 4 (n), each
-// TM/2 rows x 64 weight rows (MT = TM/32, NT = 4 tiles of 16x16); K steps of 128 through a direct-to-
-// LDS ring of as many stages as LDS holds (3 for TM <= 128, 2 for 256), with the swizzled LDS tiles,
-// load schedule and fold of the dense LDS kernel. GATEUP orders the tile's 256 weight rows as
-// (gate 16, up 16) pairs over 128 intermediate columns, so tiles nt = 2q and 2q + 1 of a wave are
-// the gate and the up of the same 16 columns.
+// One work item: a TM-row block (class TM of the block table) x 256 weight rows; 8 waves in 2 (m) x 4
+// (n), each TM/2 rows x 64 weight rows (MT = TM/32, NT = 4 tiles of 16x16); K steps of 128 through a
+// direct-to-LDS ring of as many stages as LDS holds (3 for TM <= 128, 2 for 256), with the swizzled
+// LDS tiles, load schedule and fold of the dense LDS kernel. GATEUP orders the tile's 256 weight rows
+// as (gate 16, up 16) pairs over 128 intermediate columns, so tiles nt = 2q and 2q + 1 of a wave are
+// the gate and the up of the same 16 columns. LDS comes from the caller's buffer (moe_smem_bytes).
+template <int TM>
+struct MoeSmem {
+  static constexpr int S = TM == 256 ? 2 : 3, MT = TM / 32;
+  static constexpr int kStageA = TM * 128, kStageB = kTN * 128;
+  static constexpr int kA = 0, kB = kA + S * kStageA, kS = kB + S * kStageB, kDummy = kS + S * TM * 4,
+                       kSB = kDummy + 8 * 64 * 4, kAmax = kSB + 2 * 512 * 4, kBytes = kAmax + 2 * MT * 16 * 4 * 4;
+};
+constexpr int kMoeSmemBytes =
+    MoeSmem<256>::kBytes > MoeSmem<128>::kBytes
+        ? (MoeSmem<256>::kBytes > MoeSmem<64>::kBytes ? MoeSmem<256>::kBytes : MoeSmem<64>::kBytes)
+        : (MoeSmem<128>::kBytes > MoeSmem<64>::kBytes ? MoeSmem<128>::kBytes : MoeSmem<64>::kBytes);
+static_assert(kMoeSmemBytes <= 160 * 1024, "LDS");
+
 template <int MODE, bool PRE, int TM>
-__global__ __launch_bounds__(512) void moe_gemm_kernel(MoeGemmArgs p) {
-  constexpr int TN = kTN, S = TM == 256 ? 2 : 3;
+__device__ __forceinline__ void moe_item(const MoeGemmArgs& p, uint8_t* smem, int cls, int blk, int pn) {
+  using L = MoeSmem<TM>;
+  constexpr int TN = kTN, S = L::S;
   constexpr int MT = TM / 32, NT = TN / 64;
   constexpr int AI = TM / 64, BI = TN / 64;
   constexpr int kLoads = AI + BI + 1;
   constexpr int kScaleWaves = TM / 64;
-  constexpr int kStageA = TM * 128, kStageB = TN * 128;
-  __shared__ __attribute__((aligned(1024))) uint8_t sA[S * kStageA];
-  __shared__ __attribute__((aligned(1024))) uint8_t sB[S * kStageB];
-  __shared__ __attribute__((aligned(16))) float sS[S * TM];
-  __shared__ __attribute__((aligned(16))) float sDummy[8 * 64];
-  __shared__ float sSB[2][512];
-  __shared__ float sAmax[2][MT][16][4];
+  constexpr int kStageA = L::kStageA, kStageB = L::kStageB;
+  uint8_t* sA = smem + L::kA;
+  uint8_t* sB = smem + L::kB;
+  float* sS = reinterpret_cast<float*>(smem + L::kS);
+  float* sDummy = reinterpret_cast<float*>(smem + L::kDummy);
+  float (*sSB)[512] = reinterpret_cast<float (*)[512]>(smem + L::kSB);
+  float (*sAmax)[MT][16][4] = reinterpret_cast<float (*)[MT][16][4]>(smem + L::kAmax);
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -380,13 +397,9 @@ __global__ __launch_bounds__(512) void moe_gemm_kernel(MoeGemmArgs p) {
   const int c = lp ^ lr;
   const int KB = p.K >> 7;
   const int64_t kt32 = p.K >> 5;
-  const int nblk = *p.nblk;
-  const int items = nblk * p.tiles_n;
-
-  for (int item = blockIdx.x; item < items; item += gridDim.x) {
-    __syncthreads();  // every wave is done with the previous item's LDS
-    const int blk = item % nblk, pn = item / nblk;
-    const int e = p.blk_expert[blk], row0 = p.blk_row[blk], rows = p.blk_rows[blk];
+  {
+    const int bi = cls * p.blk_cap + blk;
+    const int e = p.blk_expert[bi], row0 = p.blk_row[bi], rows = p.blk_rows[bi];
 
     // A: wave w moves tile rows [w*TM/8, (w+1)*TM/8) in slabs of 8; waves below kScaleWaves also move
     // a_scale rows [64w, 64w + 64), the others an empty load (same count per wave).
@@ -569,6 +582,37 @@ __global__ __launch_bounds__(512) void moe_gemm_kernel(MoeGemmArgs p) {
   }
 }
 
+// Grouped GEMM over all three block classes in one persistent launch. Workgroups claim work items from
+// a ticket counter; the claim order spreads the 256-row items (large experts, MFMA-bound) evenly
+// among the 128- and 64-row items (small experts, bound by their weight stream), so at any time some
+// CUs run each kind and the two overlap instead of running one after the other. A workgroup leaves
+// once its ticket is past the last item.
+template <int MODE, bool PRE>
+__global__ __launch_bounds__(512) void moe_gemm_kernel(MoeGemmArgs p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kMoeSmemBytes];
+  __shared__ int ticket;
+  const int tn = p.tiles_n;
+  const int n0 = p.nblk[0], n1 = p.nblk[1], n2 = p.nblk[2];
+  const int heavy = n0 * tn, c1 = n1 * tn, items = heavy + c1 + n2 * tn;
+  for (;;) {
+    __syncthreads();  // every wave is done with the previous item's LDS and has read the ticket
+    if (threadIdx.x == 0) ticket = atomicAdd(p.tickets, 1);
+    __syncthreads();
+    const int t = ticket;
+    if (t >= items) break;
+    const int hk = (int)((int64_t)t * heavy / items);  // 256-row items before ticket t
+    if ((int64_t)(t + 1) * heavy / items > hk) {
+      moe_item<MODE, PRE, 256>(p, smem, 0, hk % n0, hk / n0);
+    } else {
+      const int i = t - hk;
+      if (i < c1)
+        moe_item<MODE, PRE, 128>(p, smem, 1, i % n1, i / n1);
+      else
+        moe_item<MODE, PRE, 64>(p, smem, 2, (i - c1) % n2, (i - c1) / n2);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // combine: out[t] = bf16(sum over slots in slot order of weight * y[row]); 8 columns per thread.
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y, const int32_t* __restrict__ row_of,
@@ -598,7 +642,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
 // ---------------------------------------------------------------------------------------------
 // host side
 struct Workspace {
-  size_t logits, ids, weights, row_of, sorted_tok, blk_expert, blk_row, blk_rows, nblk, xq, xs, hq, hs, y, total;
+  size_t logits, ids, weights, row_of, sorted_tok, blk_expert, blk_row, blk_rows, nblk, tickets, xq, xs, hq, hs, y,
+      total;
   int blk_cap;  // block-table entries per class
 };
 
@@ -627,6 +672,7 @@ static Workspace layout(int64_t T, int64_t S, int64_t D, int64_t I, int64_t E, i
   w.blk_row = take((size_t)maxblk * 4);
   w.blk_rows = take((size_t)maxblk * 4);
   w.nblk = take(4 * kClasses);
+  w.tickets = take(4 * 2);
   w.xq = take((size_t)(T * D));
   w.xs = take((size_t)(D / 128 * T * 4));
   w.hq = take((size_t)(R * I));
@@ -656,30 +702,11 @@ static bool dims_ok(int64_t T, int64_t D, int64_t I, int64_t E, int64_t S) {
   return R * D * 2 < 0x7FFFFFFFll && R * I < 0x7FFFFFFFll && T * D < 0x7FFFFFFFll;
 }
 
-template <int MODE, bool PRE>
-static void launch_classes(MoeGemmArgs a, const BlockTable& bt, hipStream_t stream) {
-  const dim3 grid((unsigned)num_cus());
-  a.blk_expert = bt.expert;
-  a.blk_row = bt.row;
-  a.blk_rows = bt.rows;
-  a.nblk = bt.count;
-  hipLaunchKernelGGL((moe_gemm_kernel<MODE, PRE, 256>), grid, dim3(512), 0, stream, a);
-  a.blk_expert += bt.cap;
-  a.blk_row += bt.cap;
-  a.blk_rows += bt.cap;
-  a.nblk += 1;
-  hipLaunchKernelGGL((moe_gemm_kernel<MODE, PRE, 128>), grid, dim3(512), 0, stream, a);
-  a.blk_expert += bt.cap;
-  a.blk_row += bt.cap;
-  a.blk_rows += bt.cap;
-  a.nblk += 1;
-  hipLaunchKernelGGL((moe_gemm_kernel<MODE, PRE, 64>), grid, dim3(512), 0, stream, a);
-}
-
 template <bool PRE>
-static void launch_gemms(const MoeGemmArgs& gu, const MoeGemmArgs& dn, const BlockTable& bt, hipStream_t stream) {
-  launch_classes<kGateUp, PRE>(gu, bt, stream);
-  launch_classes<kDown, PRE>(dn, bt, stream);
+static void launch_gemms(const MoeGemmArgs& gu, const MoeGemmArgs& dn, hipStream_t stream) {
+  const dim3 grid((unsigned)num_cus());
+  hipLaunchKernelGGL((moe_gemm_kernel<kGateUp, PRE>), grid, dim3(512), 0, stream, gu);
+  hipLaunchKernelGGL((moe_gemm_kernel<kDown, PRE>), grid, dim3(512), 0, stream, dn);
 }
 
 // Experts on a routing already in ids/weights ([T, S], slots in [0, E); others are skipped).
@@ -701,8 +728,10 @@ static int run_experts(const uint16_t* hidden, int64_t T, int64_t D, int64_t I, 
   uint8_t* hq = ws + L.hq;
   float* hs = reinterpret_cast<float*>(ws + L.hs);
   uint16_t* y = reinterpret_cast<uint16_t*>(ws + L.y);
+  int* tickets = reinterpret_cast<int*>(ws + L.tickets);
 
-  hipLaunchKernelGGL(align_kernel, dim3(1), dim3(1024), 0, stream, ids, (int)R, (int)S, (int)E, row_of, sorted_tok, bt);
+  hipLaunchKernelGGL(align_kernel, dim3(1), dim3(1024), 0, stream, ids, (int)R, (int)S, (int)E, row_of, sorted_tok, bt,
+                     tickets);
   const int64_t qgroups = T * (D / 128);
   hipLaunchKernelGGL(quant_div_kernel, dim3((unsigned)((qgroups + 15) / 16)), dim3(256), 0, stream, hidden, (int)T,
                      (int)D, xq, xs);
@@ -722,6 +751,12 @@ static int run_experts(const uint16_t* hidden, int64_t T, int64_t D, int64_t I, 
   gu.hq = hq;
   gu.hs = hs;
   gu.R = R;
+  gu.blk_expert = bt.expert;
+  gu.blk_row = bt.row;
+  gu.blk_rows = bt.rows;
+  gu.nblk = bt.count;
+  gu.blk_cap = bt.cap;
+  gu.tickets = tickets;
   MoeGemmArgs dn = gu;
   dn.a = hq;
   dn.sa = hs;
@@ -735,10 +770,11 @@ static int run_experts(const uint16_t* hidden, int64_t T, int64_t D, int64_t I, 
   dn.N = (int)D;
   dn.tiles_n = (int)((D + kTN - 1) / kTN);
   dn.y = y;
+  dn.tickets = tickets + 1;
   if (w_layout == AKLR_B_PRESHUFFLE_16x16)
-    launch_gemms<true>(gu, dn, bt, stream);
+    launch_gemms<true>(gu, dn, stream);
   else
-    launch_gemms<false>(gu, dn, bt, stream);
+    launch_gemms<false>(gu, dn, stream);
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)T), dim3(256), 0, stream, y, row_of, weights, (int)S, (int)D, out);
   AKLR_LAUNCH_CHECK();
   return AKLR_OK;
