@@ -16,7 +16,7 @@ roofline.traffic: HBM bytes per launch of that kernel from two rocprofv3 --pmc r
 WRITE_SIZE) of ``python3 bench.py --probe-traffic``, each scaled by what the counter reads for a plain
 copy of known size in the same run; read from the committed profiles/ summary (null when absent).
 prefill / mxfp4: extra figures (TFLOP/s vs the dense FP8 5.0 PF / MXFP4 10.1 PF peaks): FP8 at
-M in {1024, 4096, 8192}, MXFP4 at M in {1, 4096}.
+M in {1024, 4096, 8192}, MXFP4 at M in {1, 32, 512, 4096} (M <= 32 as GB/s vs 8 TB/s).
 moe: the grouped DeepSeek-V3 FP8 MoE experts (256 routed + 1 shared, top-8,
 D=7168, I=2048, e4m3 weights with 128x128 scales) on Zipf(1.1) routing at T in {64, 4096}: time per
 call, touched-weight bytes / time vs 8 TB/s, and TFLOP/s vs 5.0 PF.
@@ -160,13 +160,13 @@ def mxfp4_figures(dev, stream, steps=10):
     from aklr_amd import layouts, workloads
 
     out = []
-    for m in (1, 4096):
+    for m in workloads.MXFP4_M:  # m <= 32 reported against HBM, m >= 512 against the MXFP4 MFMA peak
         for (n, k) in workloads.LLAMA70B_NK:
             x = workloads.activations(m, k, seed=1, device=dev)
             qa, sa = aklr_amd.dynamic_mxfp4_quant(x, shuffle=True)
             per = gemm4_bytes(0, n, k)
             copies = []
-            for r in range(_copies(per, lo=2) if m == 1 else 1):
+            for r in range(_copies(per, lo=2) if m <= 32 else 1):
                 wb, sb = workloads.mxfp4_weight(n, k, seed=10 + r, device=dev)
                 copies.append((layouts.shuffle_weight(wb), layouts.e8m0_scales(sb)))
 
@@ -177,7 +177,7 @@ def mxfp4_figures(dev, stream, steps=10):
             g = _capture(run, stream)
             t = _replay_time_ms([g], steps, 2, stream) / len(copies)
             rec = {"m": m, "n": n, "k": k, "us": round(t * 1e3, 2)}
-            if m == 1:
+            if m <= 32:
                 gbs = gemm4_bytes(m, n, k) / (t * 1e-3) / 1e9
                 rec.update(gbs=round(gbs, 1), frac_hbm_peak=round(gbs / HBM_PEAK_GBS, 4))
             else:
