@@ -74,6 +74,19 @@ __device__ __forceinline__ void buf_ld_lds4(rsrc_t r, void* lds, uint32_t voffse
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 4, (int)voffset, 0, 0, 0);
 }
 
+// Byte extent for a buffer descriptor, clamped to the 31-bit range raw buffer offsets address.
+__device__ __forceinline__ uint32_t rsrc_bytes(int64_t bytes) {
+  return (uint32_t)(bytes > 0x7FFFFFFFll ? 0x7FFFFFFFll : (bytes < 0 ? 0 : bytes));
+}
+
+// Workgroup barrier fenced for LDS only (s_waitcnt lgkmcnt(0) + s_barrier): global loads in flight,
+// such as a register ring of weight tiles, stay in flight across it.
+__device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // fl32(1/448) = 0x3B124925 (0x1.24924ap-9): the e4m3fn quantizer multiplies amax by this constant
 // (it does not divide by 448).
 constexpr float kInv448 = 0x1.24924ap-9f;

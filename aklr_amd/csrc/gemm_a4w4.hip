@@ -6,10 +6,12 @@
 // scale of that row and 32-block, and the atom applies the scales itself. No VALU fold: the MFMA
 // accumulates straight into the fp32 result.
 //
-// * skinny (m <= 32): weight streaming, as the FP8 skinny kernel -- a workgroup owns 32 columns and a
-//   K range, each wave a contiguous K sub-range with a register ring; fixed-order wave reduction in
-//   LDS, then (when K is also split across workgroups) fp32 partials summed in split order by the
-//   last workgroup to arrive.
+// * skinny (m <= 16, and 16 < m <= 32 with unaligned row-major scales): weight streaming -- a
+//   workgroup owns 32 columns and a K range, each wave a contiguous K sub-range with a register ring;
+//   fixed-order wave reduction in LDS, then (when K is also split across workgroups) fp32 partials
+//   summed in split order by the last workgroup to arrive.
+// * stream (16 < m <= 32): the FP8 stream kernel's design -- compute waves stream their own weight
+//   columns into register rings while a loader wave stages A and its scales in LDS for all of them.
 // * lds (m > 32, k % 256 == 0): the FP8 LDS kernel's tiles and direct-to-LDS ring, K steps of 256
 //   values with the scale bytes staged beside the codes (see gemm4_lds_kernel).
 // * tile (m > 32, other k): 128x128 tiles, 4 waves of 64x64, K steps of 256 (128 bytes per row)
@@ -58,7 +60,7 @@ __device__ __forceinline__ i32x8 fp4_frag(const u32x4& v) {
 constexpr int kFp4 = 4;
 
 // ---------------------------------------------------------------------------------------------
-// skinny (m <= 32): weight streaming, the FP8 skinny kernel's design (gemm_a8w8.hip). A workgroup owns
+// skinny (m <= 32): weight streaming. A workgroup owns
 // 16 * NT output columns and a K range (split across workgroups when the columns alone leave the chip
 // idle); each of its NW waves streams its own contiguous sub-range of 128-value K steps straight from
 // HBM into MFMA operand registers through raw buffer loads, a D-deep register ring, steps past the
@@ -232,6 +234,245 @@ __global__ __launch_bounds__(NW * 64) void gemm4_skinny_kernel(Gemm4Args p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       if (row0 + r < p.m) store_out(p.out, (int64_t)(row0 + r) * p.ldo + col, v[r] + bv, p.out_dtype);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// stream (16 < m <= 32): the FP8 stream kernel's design (gemm_a8w8.hip) on e2m1. A workgroup owns
+// NW * NT * 16 output columns and a K range of 256-value blocks (128 bytes of codes per row). Its NW
+// compute waves stream their NT weight tiles from HBM straight into a D-deep register ring (codes and
+// the tiles' e8m0 scales); one loader wave moves each K block of A -- the codes in MFMA fragment order
+// (1 KiB chunk (mt, h): lane l's 16 bytes are row mt * 16 + l % 16, bytes 64h + 16 (l / 16) of the
+// block) and the rows' 8 scale bytes, 256 bytes per 32 rows in the caller's layout -- into an
+// NS-stage LDS ring. One LDS-fenced barrier per block hands a stage over; the MFMA applies both
+// scales, so there is no fold. Lane groups past k load zero codes and take scale 1.0, so padding scale
+// bytes never reach the MFMA. Row-major scales need 4-byte-aligned rows (stream4_ok).
+template <int NT>
+struct Stream4Frag {
+  u32x4 b[NT][2];
+  uint32_t sb[NT];  // shuffled: the tile row's dword (both K steps, both 16-row halves); row-major: 2 bytes
+};
+
+template <int MT, int NT, int NW, int D, int NS, bool PRE, bool SSHUF>
+__global__ __launch_bounds__((NW + 1) * 64) void gemm4_stream_kernel(Gemm4Args p) {
+  static_assert(NS >= 2 && D >= 1 && MT >= 1 && MT <= 8 && 128 % (NT * 16) == 0, "stream shape");
+  constexpr int kSGroups = MT >= 2 ? MT / 2 : 1;     // 32-row scale groups per stage
+  constexpr int kLoadsA = 2 * MT + kSGroups;         // loader loads per stage
+  constexpr int kCols = NW * NT * 16;
+  static_assert((NS - 2) * kLoadsA <= 63, "the loader's wait count must fit vmcnt");
+  __shared__ __attribute__((aligned(1024))) uint8_t sA[NS][MT * 2048];
+  __shared__ __attribute__((aligned(16))) uint8_t sS[NS][kSGroups * 256];
+  __shared__ unsigned arrive_slot;
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * kCols;
+  const int split = blockIdx.y;
+  const int KB = (p.k + 255) >> 8;  // 256-value blocks
+  const int kb_begin = split * p.ks_per_split;
+  const int kb_end = min(KB, kb_begin + p.ks_per_split);
+  const int64_t kbytes = p.k >> 1, kt32 = kbytes >> 5;
+  const int kcols = p.k >> 5;  // scale columns
+  const int64_t c8 = p.pc >> 3;
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int c0w = n0 + w * NT * 16;
+  const int col_w = c0w + 4 * g;
+  const int64_t plane = (int64_t)gridDim.x * NW * MT * NT * 256;  // split-K partials, accumulator order
+  const int64_t part_base = ((int64_t)blockIdx.x * NW + w) * (MT * NT) * 256 + lane * 4;
+
+  if (w == NW) {
+    // Loader. Rows past m and byte granules past k read the out-of-range offset (zeros).
+    const i32x4 ars = make_rsrc_words(p.a, rsrc_bytes((int64_t)(p.m - 1) * p.lda + kbytes));
+    const i32x4 sars = SSHUF ? make_rsrc_words(p.sa, rsrc_bytes((int64_t)p.pr_a * p.pc))
+                             : make_rsrc_words(p.sa, rsrc_bytes((int64_t)(p.m - 1) * p.lds_a + kcols));
+    uint32_t a_off[MT], s_off[kSGroups];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int row = mt * 16 + li;
+      a_off[mt] = row < p.m ? (uint32_t)((int64_t)row * p.lda + g * 16) : kOobOffset;
+    }
+#pragma unroll
+    for (int r = 0; r < kSGroups; ++r) {
+      if (SSHUF) {
+        s_off[r] = (uint32_t)((int64_t)r * c8 * 256 + lane * 4);
+      } else {
+        const int row = r * 32 + (lane >> 1);
+        s_off[r] = row < p.m ? (uint32_t)((int64_t)row * p.lds_a + (lane & 1) * 4) : kOobOffset;
+      }
+    }
+    const uint32_t lds_a0 = lds_addr(&sA[0][0]), lds_s0 = lds_addr(&sS[0][0]);
+    auto issue = [&](int kb, int st) {
+      const bool on = kb < kb_end;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int64_t byte = (int64_t)kb * 128 + 64 * h + g * 16;  // this lane's granule along the row
+          lds_dma16(ars, lds_a0 + st * (MT * 2048) + mt * 2048 + h * 1024,
+                    on && byte < kbytes && a_off[mt] != kOobOffset ? a_off[mt] + (uint32_t)(kb * 128 + 64 * h) : kOobOffset);
+        }
+#pragma unroll
+      for (int r = 0; r < kSGroups; ++r)
+        lds_dma4(sars, lds_s0 + st * (kSGroups * 256) + r * 256,
+                 on && s_off[r] != kOobOffset ? s_off[r] + (uint32_t)kb * (SSHUF ? 256u : 8u) : kOobOffset);
+    };
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) issue(kb_begin + s, s);
+    int st_fill = NS - 1;
+    for (int kb = kb_begin; kb < kb_end; ++kb) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * kLoadsA) : "memory");
+      stage_barrier();
+      issue(kb + NS - 1, st_fill);
+      st_fill = st_fill + 1 == NS ? 0 : st_fill + 1;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    // Compute wave. Column tiles past n read tile 0 (never stored).
+    rsrc_t brs[NT];
+    int bcol[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int64_t c0 = (c0w + nt * 16) < p.n ? c0w + nt * 16 : 0;
+      bcol[nt] = (int)c0 + li;
+      if (PRE)
+        brs[nt] = make_rsrc(p.b + (c0 >> 4) * kt32 * 512, (uint32_t)(kt32 * 512));
+      else
+        brs[nt] = make_rsrc(p.b + c0 * p.ldb, (uint32_t)(15 * p.ldb + kbytes));
+    }
+    const uint32_t b_lane = PRE ? (uint32_t)((g >> 1) * 512 + (g & 1) * 256 + li * 16) : (uint32_t)(li * p.ldb + g * 16);
+    const rsrc_t sbrs = SSHUF ? make_rsrc(p.sb, (uint32_t)((int64_t)p.pr_b * p.pc))
+                              : make_rsrc(p.sb, (uint32_t)((int64_t)(p.n - 1) * p.lds_b + kcols));
+    uint32_t sb_base[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      sb_base[nt] = SSHUF ? (uint32_t)((((int64_t)bcol[nt] >> 5) * c8) * 256 + (g * 16 + (bcol[nt] & 15)) * 4)
+                          : (uint32_t)((int64_t)bcol[nt] * p.lds_b + g);
+    auto load = [&](int kb, Stream4Frag<NT>& f) {
+      const bool on = kb < kb_end;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const bool gr = on && (int64_t)kb * 128 + 64 * h + g * 16 < kbytes;
+        const uint32_t off = gr ? (uint32_t)(PRE ? kb * 2048 + 1024 * h : kb * 128 + 64 * h) : kOobOffset;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) f.b[nt][h] = buf_ld16<kNt>(brs[nt], off == kOobOffset ? kOobOffset : b_lane + off);
+      }
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        if (SSHUF) {
+          f.sb[nt] = buf_ld4(sbrs, on ? sb_base[nt] + (uint32_t)kb * 256u : kOobOffset);
+        } else {
+          const uint32_t o = on ? sb_base[nt] + (uint32_t)kb * 8u : kOobOffset;
+          f.sb[nt] = buf_ld1(sbrs, o) | (buf_ld1(sbrs, on ? o + 4 : kOobOffset) << 8);
+        }
+      }
+    };
+    // The scale byte of K step h of this block for lane group g; 127 (1.0) past k.
+    auto pick_b = [&](const Stream4Frag<NT>& f, int nt, int h, bool valid) {
+      const uint32_t v = SSHUF ? f.sb[nt] >> (16 * h + 8 * ((bcol[nt] >> 4) & 1)) : f.sb[nt] >> (8 * h);
+      return valid ? (int)(v & 0xFF) : 127;
+    };
+
+    int st = 0;
+    auto step = [&](int kb, Stream4Frag<NT>& f) {
+      stage_barrier();
+      const uint8_t* A = sA[st];
+      const uint8_t* S = sS[st];
+      i32x8 af[MT][2];
+      uint32_t sw[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) af[mt][h] = fp4_frag(*reinterpret_cast<const u32x4*>(A + mt * 2048 + h * 1024 + lane * 16));
+        const int row = mt * 16 + li;
+        if (SSHUF) {
+          sw[mt] = *reinterpret_cast<const uint32_t*>(S + (row >> 5) * 256 + (g * 16 + (row & 15)) * 4);
+        } else {
+          const uint8_t* rs = S + (row >> 5) * 256 + (row & 31) * 8 + g;
+          sw[mt] = (uint32_t)rs[0] | ((uint32_t)rs[4] << 8);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const bool valid = (kb * 2 + h) * 4 + g < kcols;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const uint32_t v = SSHUF ? sw[mt] >> (16 * h + 8 * (mt & 1)) : sw[mt] >> (8 * h);
+          const int asc = valid ? (int)(v & 0xFF) : 127;
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            acc[mt][nt] = mfma16x128_scaled<kFp4, 0, 0>(fp4_frag(f.b[nt][h]), af[mt][h], acc[mt][nt],
+                                                          pick_b(f, nt, h, valid), asc);
+        }
+      }
+      load(kb + D, f);
+      __builtin_amdgcn_sched_barrier(0);  // refill this slot before consuming the next
+      st = st + 1 == NS ? 0 : st + 1;
+    };
+
+    Stream4Frag<NT> f[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) load(kb_begin + j, f[j]);
+    const int len = kb_end - kb_begin, full = len / D * D;
+    for (int kb0 = kb_begin; kb0 < kb_begin + full; kb0 += D) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) step(kb0 + j, f[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < D - 1; ++j)
+      if (full + j < len) step(kb_begin + full + j, f[j]);
+    if (p.splits > 1) {
+      const rsrc_t prs = partial_rsrc(p.partial, split, plane);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) store_partial4(prs, part_base + (mt * NT + nt) * 256, acc[mt][nt]);
+    }
+  }
+
+  if (p.splits > 1) {
+    if (!splitk_arrive(p.counters + blockIdx.x, p.splits, &arrive_slot)) return;
+    if (w == NW) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < p.splits; ++sp) {
+      const rsrc_t r = partial_rsrc(p.partial, sp, plane);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          acc[mt][nt] += __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)((part_base + (mt * NT + nt) * 256) * 4), 0, kSc1));
+    }
+  }
+  if (w == NW) return;
+
+  // Output: a lane holds 4 consecutive columns of one row per tile; 8 bytes per tile and row.
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int col = col_w + nt * 16;
+    if (col >= p.n) continue;
+    f32x4 bx = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bx[r] = p.bias[col + r];
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int row = mt * 16 + li;
+      if (row >= p.m) continue;
+      const f32x4 x = acc[mt][nt] + bx;
+      const u32x2 v = {pack_out2(x[0], x[1], p.out_dtype), pack_out2(x[2], x[3], p.out_dtype)};
+      *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + col) = v;
+    }
   }
 }
 
@@ -639,6 +880,49 @@ static void launch_skinny4(const Gemm4Args& g, const Skinny4Plan& p, hipStream_t
   else launch_skinny4<2, 2, PRE, SSHUF>(g, p, s);
 }
 
+// Stream plan for 16 < m <= 32 (two row tiles; measured on MI355X over the Llama-70B MXFP4 shapes,
+// where the stream kernel beats the skinny kernel by 18-20% at m = 32 but not at m = 1, and the LDS
+// kernel from m = 64): 4 compute waves of one column tile each, or 8 waves of two once n >= 32768;
+// ring depth 2; K split in 2 or 4 (a power of two) until about 2048 compute waves run. Row-major
+// scales need 4-byte-aligned rows (direct-to-LDS loads of whole dwords).
+static constexpr int64_t kStream4MinM = 17;
+
+struct Stream4Plan {
+  int nt, nw, groups, splits, ks_per_split;
+};
+
+static Stream4Plan plan_stream4(int64_t n, int64_t k) {
+  Stream4Plan p;
+  p.nt = n >= 32768 ? 2 : 1;
+  p.nw = p.nt == 2 ? 8 : 4;
+  p.groups = (int)((n + 16 * p.nt * p.nw - 1) / (16 * p.nt * p.nw));
+  const int64_t KB = (k + 255) / 256;
+  int64_t s = 1;
+  while (s < 4 && (int64_t)p.groups * p.nw * s * 2 <= 2048 && KB >= 8 * s) s *= 2;
+  if (p.groups > kSplitkMaxTiles) s = 1;
+  p.ks_per_split = (int)((KB + s - 1) / s);
+  p.splits = (int)((KB + p.ks_per_split - 1) / p.ks_per_split);
+  return p;
+}
+
+static size_t stream4_partial_bytes(const Stream4Plan& p) {
+  return (size_t)p.splits * (size_t)p.groups * p.nw * 2 * p.nt * 1024;
+}
+
+static bool stream4_ok(int64_t m, int scale_layout, int64_t lds_a, const uint8_t* sa) {
+  if (m < kStream4MinM || m > kDecode4MaxM) return false;
+  return scale_layout == AKLR_SCALES_SHUFFLED || (lds_a % 4 == 0 && (reinterpret_cast<uintptr_t>(sa) & 3u) == 0);
+}
+
+template <bool PRE, bool SSHUF>
+static void launch_stream4(const Gemm4Args& g, const Stream4Plan& p, hipStream_t s) {
+  const dim3 grid((unsigned)p.groups, (unsigned)p.splits);
+  if (p.nt == 2)
+    hipLaunchKernelGGL((gemm4_stream_kernel<2, 2, 8, 2, 4, PRE, SSHUF>), grid, dim3(9 * 64), 0, s, g);
+  else
+    hipLaunchKernelGGL((gemm4_stream_kernel<2, 1, 4, 2, 4, PRE, SSHUF>), grid, dim3(5 * 64), 0, s, g);
+}
+
 // LDS-kernel plan for m > 32 when k % 256 == 0 (and, for row-major scales, 4-byte aligned scale rows):
 // tile and split count by the FP8 LDS kernel's cost model (per-K-step times per tile shape, rounds of
 // 256 workgroups, only 128x128 tiles split K).
@@ -717,9 +1001,14 @@ static size_t lds4_partial_bytes(const Lds4Plan& p) {
 
 extern "C" size_t aklr_gemm_a4w4_mxfp4_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k < 64) return 0;
-  if (m <= kDecode4MaxM) {
+  if (m <= kDecode4MaxM) {  // the stream kernel may be declined at call time: cover the skinny kernel too
     const Skinny4Plan d = plan_skinny4(m, n, k);
-    return d.splits > 1 ? kSplitkCounterBytes + (size_t)d.splits * (size_t)round4(m) * (size_t)n * sizeof(float) : 0;
+    size_t need = d.splits > 1 ? (size_t)d.splits * (size_t)round4(m) * (size_t)n * sizeof(float) : 0;
+    if (m >= kStream4MinM) {
+      const Stream4Plan sp = plan_stream4(n, k);
+      if (sp.splits > 1 && stream4_partial_bytes(sp) > need) need = stream4_partial_bytes(sp);
+    }
+    return need ? kSplitkCounterBytes + need : 0;
   }
   if (k % 256 != 0) return 0;
   const Lds4Plan lp = plan_lds4(m, n, k);
@@ -770,6 +1059,22 @@ extern "C" int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t
   g.pr_a = (int)((m + 255) / 256 * 256);
   g.pr_b = (int)((n + 255) / 256 * 256);
 
+  if (stream4_ok(m, scale_layout, lds_a, a_scale)) {
+    const Stream4Plan sp = plan_stream4(n, k);
+    g.splits = sp.splits;
+    g.ks_per_split = sp.ks_per_split;
+    if (sp.splits > 1) {
+      const size_t need = kSplitkCounterBytes + stream4_partial_bytes(sp);
+      if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) return AKLR_ERR_WORKSPACE;
+      g.counters = static_cast<unsigned*>(workspace);
+      g.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kSplitkCounterBytes);
+    }
+    const bool sshuf = scale_layout == AKLR_SCALES_SHUFFLED;
+    if (g.b_pre) sshuf ? launch_stream4<true, true>(g, sp, stream) : launch_stream4<true, false>(g, sp, stream);
+    else sshuf ? launch_stream4<false, true>(g, sp, stream) : launch_stream4<false, false>(g, sp, stream);
+    AKLR_LAUNCH_CHECK();
+    return AKLR_OK;
+  }
   if (m <= kDecode4MaxM) {
     const Skinny4Plan d = plan_skinny4(m, n, k);
     g.splits = d.splits;

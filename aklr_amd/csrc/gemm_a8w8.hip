@@ -54,16 +54,6 @@ struct Gemm8Args {
 // sides' wait counts are exact: the loader waits for its own stage with an immediate count, and the
 // compiler tracks the weight ring. One barrier per K block, fenced for LDS only, hands a stage from
 // the loader to the compute waves and the consumed slot back, without draining the weight ring.
-__device__ __forceinline__ uint32_t rsrc_bytes(int64_t bytes) {
-  return (uint32_t)(bytes > 0x7FFFFFFFll ? 0x7FFFFFFFll : (bytes < 0 ? 0 : bytes));
-}
-
-__device__ __forceinline__ void stage_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 template <int NT>
 struct StreamFrag {
   i32x8 b[NT];

@@ -296,7 +296,7 @@ def gemm_a4w4_mxfp4(
     if not workspace.ready(a.device, _lib.lib().aklr_gemm_a4w4_mxfp4_workspace_bytes(m, n, k)):
         return FallbackReason.NOT_WARMED
     pre = variant == "b_shuffled"
-    path = "decode" if m <= 32 else "tile"
+    path = "skinny" if m <= 16 else ("stream" if m <= 32 else "lds")  # as the library picks (aligned scales)
     return _Gemm4Plan(a, b, a_scale, b_scale, bias, out, dt, m, n, k,
                       _lib.B_PRESHUFFLE_16x16 if pre else _lib.B_ROW_MAJOR,
                       _lib.SCALES_SHUFFLED if pre else _lib.SCALES_ROW_MAJOR, variant,

@@ -206,7 +206,8 @@ def test_mxfp4_llama(m, nk, shuffled):
 
 @pytest.mark.parametrize("m,n,k", [(1, 16, 64), (3, 32, 192), (33, 48, 320), (200, 272, 64), (40, 160, 4160),
                                    (33, 48, 256), (129, 16, 512), (300, 272, 1024), (700, 400, 2048),
-                                   (2100, 1040, 768), (1, 160, 16448), (7, 48, 20032)])
+                                   (2100, 1040, 768), (1, 160, 16448), (7, 48, 20032), (20, 48, 320),
+                                   (32, 160, 4160), (25, 4112, 1024), (32, 40960, 512)])
 def test_mxfp4_small_and_ragged_k(m, n, k):
     _mxfp4_run(m, n, k, shuffled=True, seed=m, bias=True)
     _mxfp4_run(m, n, k, shuffled=False, seed=m + 1)
