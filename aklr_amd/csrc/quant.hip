@@ -145,13 +145,19 @@ __global__ __launch_bounds__(256) void quant_mxfp8_kernel(const uint16_t* __rest
   }
 }
 
-// e2m1 index of |v| (v already divided by the block scale, |v| <= 6): nearest grid point of
-// {0, .5, 1, 1.5, 2, 3, 4, 6}, ties to the even index -- strict '>' where the tie goes down,
-// '>=' where it goes up.
-__device__ __forceinline__ uint32_t e2m1_code(float v) {
-  const float m = fabsf(v);
-  uint32_t idx = (m > 0.25f) + (m >= 0.75f) + (m > 1.25f) + (m >= 1.75f) + (m > 2.5f) + (m >= 3.5f) + (m > 5.0f);
-  return idx | ((__float_as_uint(v) >> 28) & 8u);
+// e2m1 codes of 8 values already divided by the block scale (|v| <= 6): the nearest grid point of
+// {0, .5, 1, 1.5, 2, 3, 4, 6}, ties to the even code, sign kept (also on zero) -- what
+// V_CVT_SCALEF32_PK_FP4_F32 computes at scale 1.0, two values per instruction, into the byte `sel`
+// (first value in the low nibble). On this GPU it agrees with the comparison rule (codes 0..7 at
+// |v| > .25, >= .75, > 1.25, >= 1.75, > 2.5, >= 3.5, > 5) on every bf16 value of magnitude <= 6 in
+// either operand; the inputs here are bf16 values times a power of two, so that covers them all.
+__device__ __forceinline__ uint32_t e2m1_pack8(const float (&f)[8], float mul) {
+  uint32_t p = 0;
+  p = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(p, f[0] * mul, f[1] * mul, 1.0f, 0);
+  p = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(p, f[2] * mul, f[3] * mul, 1.0f, 1);
+  p = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(p, f[4] * mul, f[5] * mul, 1.0f, 2);
+  p = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(p, f[6] * mul, f[7] * mul, 1.0f, 3);
+  return p;
 }
 
 // Byte offset of scale (row, col) in aiter's shuffled e8m0 layout over a [pr, pc] padded matrix:
@@ -203,8 +209,7 @@ __global__ __launch_bounds__(256) void quant_mxfp4_kernel(const uint16_t* __rest
         // x / 2^E == x * 2^-E exactly (2^-E is representable for E in [-127, 127]; 2^-127 is the
         // subnormal 0x00400000).
         const float mul = E < 127 ? __uint_as_float((uint32_t)(127 - E) << 23) : __uint_as_float(0x00400000u);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) packed |= e2m1_code(gv.f[t] * mul) << (4 * t);
+        packed = e2m1_pack8(gv.f, mul);
         sbyte = (uint32_t)(E + 127);
       } else {
         sbyte = 255u;
