@@ -17,6 +17,8 @@ WRITE_SIZE) of ``python3 bench.py --probe-traffic``, each scaled by what the cou
 copy of known size in the same run; read from the committed profiles/ summary (null when absent).
 prefill / mxfp4: extra figures (TFLOP/s vs the dense FP8 5.0 PF / MXFP4 10.1 PF peaks): FP8 at
 M in {1024, 4096, 8192}, MXFP4 at M in {1, 32, 512, 4096} (M <= 32 as GB/s vs 8 TB/s).
+quant: the three activation quantizers at H=7168, T in {2048, 16384} (rows a1/a4/a5), next to the
+reference's recorded times where it has them.
 moe: the grouped DeepSeek-V3 FP8 MoE experts (256 routed + 1 shared, top-8,
 D=7168, I=2048, e4m3 weights with 128x128 scales) on Zipf(1.1) routing at T in {64, 4096}: time per
 call, touched-weight bytes / time vs 8 TB/s, and TFLOP/s vs 5.0 PF.
@@ -185,6 +187,54 @@ def mxfp4_figures(dev, stream, steps=10):
                 rec.update(tflops=round(tf, 1), frac_mxfp4_peak=round(tf / MXFP4_PEAK_TFLOPS, 4))
             out.append(rec)
             del copies
+    return out
+
+
+# The reference's recorded quantizer times (BASELINE: graph replay with a 1 GiB cache flush per call).
+QUANT_REFERENCE_US = {("fp8_1x128", 16384): 55.2, ("fp8_1x128", 2048): 9.43, ("mxfp8", 16384): 51.1}
+
+
+def quant_figures(dev, stream, steps=20):
+    """Rows a1/a4/a5: the three activation quantizers at H=7168, T in {2048, 16384}, called through the C
+    ABI on 4 rotating input/output sets (cold in cache, as the reference times them)."""
+    from aklr_amd import _lib, workloads
+
+    lib = _lib.lib()
+    h, n = 7168, 4
+    out = []
+    for t in (2048, 16384):
+        xs = [workloads.activations(t, h, seed=s, device=dev) for s in range(n)]
+        q8 = [torch.empty((t, h), dtype=torch.uint8, device=dev) for _ in range(n)]
+        s8 = [torch.empty((h // 128, t), dtype=torch.float32, device=dev) for _ in range(n)]
+        sm = [torch.empty((t, h // 32), dtype=torch.uint8, device=dev) for _ in range(n)]
+        q4 = [torch.empty((t, h // 2), dtype=torch.uint8, device=dev) for _ in range(n)]
+        s4 = [torch.empty(((t + 255) // 256 * 256) * ((h // 32 + 7) // 8 * 8), dtype=torch.uint8, device=dev)
+              for _ in range(n)]
+        st = stream.cuda_stream
+        cases = (
+            ("fp8_1x128", lambda i: lib.aklr_per_group_quant_fp8(xs[i].data_ptr(), h, q8[i].data_ptr(),
+                                                                 s8[i].data_ptr(), t, h, st), 3.03125),
+            ("mxfp8", lambda i: lib.aklr_per_group_quant_mxfp8(xs[i].data_ptr(), h, q8[i].data_ptr(),
+                                                               sm[i].data_ptr(), t, h, st), 3.03125),
+            ("mxfp4", lambda i: lib.aklr_dynamic_mxfp4_quant(xs[i].data_ptr(), h, q4[i].data_ptr(), s4[i].data_ptr(),
+                                                             t, h, 1, st), 2.53125),
+        )
+        for name, fn, bpe in cases:
+            def run(fn=fn):
+                for i in range(n):
+                    fn(i)
+
+            g = _capture(run, stream)
+            ms = _replay_time_ms([g], steps, 3, stream) / n
+            gbs = t * h * bpe / (ms * 1e-3) / 1e9
+            rec = {"kernel": name, "tokens": t, "hidden": h, "us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
+                   "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+            ref = QUANT_REFERENCE_US.get((name, t))
+            if ref is not None:
+                rec["reference_us"] = ref
+            out.append(rec)
+            del g
+        del xs, q8, s8, sm, q4, s4
     return out
 
 
@@ -360,6 +410,8 @@ def main(argv=None):
         extras["prefill_fp8"] = prefill_figures(dev, stream)
         torch.cuda.empty_cache()
         extras["mxfp4"] = mxfp4_figures(dev, stream)
+        torch.cuda.empty_cache()
+        extras["quant"] = quant_figures(dev, stream)
         torch.cuda.empty_cache()
         print("[bench] MoE (config 5) figures", file=sys.stderr, flush=True)
         extras["moe_fp8_deepseek_v3"] = moe_figures(dev)
