@@ -123,14 +123,14 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
       for (int i = 0; i < kSRows / 64; ++i)
         lds_dma4(sars, lds_s0 + st * (kSRows * 4) + i * 256, on && s_off[i] != kOobOffset ? s_off[i] + sk : kOobOffset);
     };
-    // Stage kb lives in slot (kb - kb_begin) % NS. Before barrier kb the loader's own loads of stage
-    // kb have landed (NS - 2 younger stages stay in flight); after it, every compute wave is done with
-    // stage kb - 1, whose slot the next issue refills. Issues past the K range load zeros, which keeps
-    // the count exact.
-#pragma unroll
-    for (int s = 0; s < NS - 1; ++s) issue(kb_begin + s, s);
+    // Stage kb lives in slot (kb - kb_begin) % NS, and all NS slots start filled. A first barrier
+    // publishes stage kb_begin; then barrier kb publishes stage kb + 1 (the loader's own loads of it
+    // have landed, NS - 2 younger stages stay in flight), and by then every compute wave has read
+    // stage kb -- fragments are read one K block ahead -- so its slot takes stage kb + NS. Issues past
+    // the K range load zeros, which keeps the count exact.
+    issue(kb_begin, 0);
     // b_scale of the workgroup's column blocks over its K range (kb_per_split <= 512), staged once,
-    // behind the first A loads; the first stage barrier publishes it with stage 0.
+    // behind the first A stage; the first stage barrier publishes it with stage 0.
     {
       const int len = kb_end - kb_begin;
       const int last_row = (p.n - 1) >> 7;
@@ -139,12 +139,15 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
         sSB[r][kk] = p.sb[(int64_t)min((n0 >> 7) + r, last_row) * p.ldbs + kb_begin + kk];
       }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every load above has landed: the counts below are exact
-    int st_fill = NS - 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage 0 and b_scale have landed
+#pragma unroll
+    for (int s = 1; s < NS; ++s) issue(kb_begin + s, s);  // only stage loads from here: the counts are exact
+    stage_barrier();
+    int st_fill = 0;
     for (int kb = kb_begin; kb < kb_end; ++kb) {
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * kLoadsA) : "memory");
       stage_barrier();
-      issue(kb + NS - 1, st_fill);
+      issue(kb + NS, st_fill);
       st_fill = st_fill + 1 == NS ? 0 : st_fill + 1;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -169,23 +172,26 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     };
     const float* sbw = sSB[(c0w >> 7) - (n0 >> 7)];
 
-    // One K block: all MT fragment reads of the stage are issued before the first MFMA, so their LDS
-    // latency overlaps; then the weight slot is refilled with block kb + D.
-    int st = 0;
-    auto step = [&](int kb, StreamFrag<NT>& f) {
-      stage_barrier();
-      const float sb = sbw[kb - kb_begin];
-      const uint8_t* A = sA[st];
-      const float* SA = sS[st];
-      i32x8 af[MT];
-      float s[MT];
+    // Fragments are read one K block ahead: the MFMAs of block kb run on registers read during block
+    // kb - 1, and each row tile's registers take block kb + 1's fragment as soon as its MFMAs have
+    // issued, so the LDS latency hides behind the MFMAs instead of stalling them. Then the weight slot
+    // is refilled with block kb + D.
+    i32x8 af[MT];
+    float s[MT];
+    auto read_frags = [&](int mt, int slot) {
+      af[mt] = cat(*reinterpret_cast<const u32x4*>(&sA[slot][mt * 2048 + lane * 16]),
+                   *reinterpret_cast<const u32x4*>(&sA[slot][mt * 2048 + 1024 + lane * 16]));
+      s[mt] = sS[slot][mt * 16 + li];
+    };
+    stage_barrier();  // publishes stage kb_begin
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        af[mt] = cat(*reinterpret_cast<const u32x4*>(A + mt * 2048 + lane * 16),
-                     *reinterpret_cast<const u32x4*>(A + mt * 2048 + 1024 + lane * 16));
-        s[mt] = SA[mt * 16 + li];
-      }
+    for (int mt = 0; mt < MT; ++mt) read_frags(mt, 0);
+    int st = 0;  // slot of stage kb + 1 during block kb
+    auto step = [&](int kb, StreamFrag<NT>& f) {
+      stage_barrier();  // publishes stage kb + 1; every wave is done reading stage kb
       __builtin_amdgcn_sched_barrier(0);
+      st = st + 1 == NS ? 0 : st + 1;
+      const float sb = sbw[kb - kb_begin];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const float sc = s[mt] * sb;
@@ -196,10 +202,18 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(part[r], sc, acc[mt][nt][r]);
         }
+        read_frags(mt, st);  // block kb + 1 (past the K range: the zeros of an empty stage)
+      }
+      // Interleave: every MFMA after the first is followed by five VALU slots, which take the scale
+      // products and the fold FMAs of earlier MFMAs, so the fold runs while the matrix core works.
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+      for (int i = 1; i < MT * NT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
       }
       load(kb + D, f);
       __builtin_amdgcn_sched_barrier(0);  // refill this slot before consuming the next
-      st = st + 1 == NS ? 0 : st + 1;
     };
 
     // D-deep ring: block kb_begin + i lives in slot i % D. Whole groups of D blocks run in a loop with
