@@ -648,17 +648,19 @@ static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
 }
 
 // Stream plan (m <= 128; measured on MI355X over the DeepSeek-V3 shapes at m = 1, 16, 32, 64, 128,
-// where it is the fastest or within 4% of the fastest of 1-4 column tiles, 4 or 8 waves, ring depths
-// 2-4, 3-8 A stages and 1-8 K splits): 1, 2, 4 or 8 row tiles, 4 compute waves, two 16-column tiles
-// per wave once n >= 4096 (one below, for more workgroups), and K split in up to 4 parts until about
-// 256 workgroups run (each split >= 4 K blocks).
+// where it is the fastest or within 4% of the fastest of 1-4 column tiles, 2, 4 or 8 waves, ring
+// depths 2-8, 3-8 A stages and 1-8 K splits): 1, 2, 4 or 8 row tiles, 4 compute waves, two 16-column
+// tiles per wave once n >= 4096 (one below; one also at m <= 16 while that leaves at most 256
+// workgroups of columns: the narrower workgroups then need fewer K splits, so less partial traffic,
+// for the same workgroup count), and K split in up to 4 parts until about 256 workgroups run (each
+// split >= 4 K blocks).
 static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k) {
   Plan8 p;
   p.kind = Kernel8::kStream;
   p.tm = p.tn = 0;
   const int64_t KB = k / 128;
   p.mt = m <= 16 ? 1 : (m <= 32 ? 2 : (m <= 64 ? 4 : 8));
-  p.nt = n >= 4096 ? 2 : 1;
+  p.nt = n >= 4096 && (m > 16 || (n + 63) / 64 > 256) ? 2 : 1;
   p.nw = 4;
   const int64_t groups = (n + 64 * p.nt - 1) / (64 * p.nt);
   p.grid_x = (int)groups;
