@@ -196,14 +196,16 @@ QUANT_REFERENCE_US = {("fp8_1x128", 16384): 55.2, ("fp8_1x128", 2048): 9.43, ("m
 
 def quant_figures(dev, stream, steps=20):
     """Rows a1/a4/a5: the three activation quantizers at H=7168, T in {2048, 16384}, called through the C
-    ABI on 4 rotating input/output sets (cold in cache, as the reference times them)."""
+    ABI on rotating input/output sets of at least 512 MB in all, so the 256 MB last-level cache holds none
+    of them (cold, as the reference times them)."""
     from aklr_amd import _lib, workloads
 
     lib = _lib.lib()
-    h, n = 7168, 4
+    h = 7168
     out = []
     for t in (2048, 16384):
-        xs = [workloads.activations(t, h, seed=s, device=dev) for s in range(n)]
+        n = max(4, -(-(512 << 20) // (t * h * 3)))
+        xs = [workloads.activations(t, h, seed=s % 4, device=dev) for s in range(n)]
         q8 = [torch.empty((t, h), dtype=torch.uint8, device=dev) for _ in range(n)]
         s8 = [torch.empty((h // 128, t), dtype=torch.float32, device=dev) for _ in range(n)]
         sm = [torch.empty((t, h // 32), dtype=torch.uint8, device=dev) for _ in range(n)]
