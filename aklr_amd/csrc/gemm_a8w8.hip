@@ -349,8 +349,12 @@ constexpr int kLdsGroup = 8;  // tile rows per raster group
 
 template <int TM, int TN, int S, int FMT, bool PRE>
 __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
-  static_assert(TM % 64 == 0 && TN % 128 == 0 && S >= 2, "tile shape");
+  static_assert(TM % 64 == 0 && (TN == 128 || TN == 192 || TN == 256) && S >= 2, "tile shape");
   constexpr int MT = TM / 32, NT = TN / 64;  // 16x16 tiles per wave along m and n
+  // TN = 192 (for N = 2112 = 11 x 192): tiles start at multiples of 64 columns, so a wave's 48 columns
+  // can straddle two 128-column b_scale blocks, and its b_scale is taken per column tile.
+  constexpr bool kBlkPerTile = TN % 128 != 0;
+  constexpr int kNBlk = (TN + 127) / 128;  // 128-column b_scale blocks a tile spans (n0 % 128 is 0 or 64)
   constexpr int AI = TM / 64, BI = TN / 64;  // 1 KiB loads per wave per stage
   constexpr int kLoads = AI + BI + 1;        // + one a_scale load
   constexpr int kStageA = TM * 128, kStageB = TN * 128;
@@ -359,7 +363,7 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   __shared__ __attribute__((aligned(1024))) uint8_t sB[S * kStageB];
   __shared__ __attribute__((aligned(16))) float sS[S * TM];
   __shared__ __attribute__((aligned(16))) float sDummy[8 * 64];  // landing area of the empty a_scale loads
-  __shared__ float sSB[TN / 128][512];  // b_scale of the tile's 128-column blocks over its K range
+  __shared__ float sSB[kNBlk][512];  // b_scale of the tile's 128-column blocks over its K range
   __shared__ unsigned arrive_slot;
 
   const int tiles_m = (p.m + TM - 1) / TM;
@@ -439,12 +443,15 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   {
     const int len = kb_end - kb_begin;
     const int last_row = (p.n - 1) >> 7;
-    for (int i = threadIdx.x; i < (TN / 128) * len; i += 512) {
+    for (int i = threadIdx.x; i < kNBlk * len; i += 512) {
       const int r = i / len, kk = i - r * len;
       sSB[r][kk] = p.sb[(int64_t)min((n0 >> 7) + r, last_row) * p.ldbs + kb_begin + kk];
     }
   }
-  const float* sbw = sSB[(wn * (TN / 4)) >> 7];
+  const float* sbw = sSB[((n0 + wn * (TN / 4)) >> 7) - (n0 >> 7)];
+  int sb_blk[NT];  // kBlkPerTile: each column tile's block
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) sb_blk[nt] = ((n0 + wn * (TN / 4) + nt * 16) >> 7) - (n0 >> 7);
 
   // Fragment addresses: every row a lane reads is congruent to li mod 8, so the swizzle term is the
   // same for all its row tiles and each read is one base plus an immediate (tile * 2048 bytes).
@@ -465,13 +472,15 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
     for (int mt = 0; mt < MT; ++mt) {
       const i32x8 af = cat(*reinterpret_cast<const u32x4*>(A + a_row + swz_lo + mt * 2048),
                            *reinterpret_cast<const u32x4*>(A + a_row + swz_hi + mt * 2048));
-      const float s = SA[mt * 16] * sb;
+      const float sa_row = SA[mt * 16];
+      const float s = sa_row * sb;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
         const f32x4 part = mfma16x128<FMT>(bf[nt], af, z);  // lane: row li, columns 4g..4g+3
+        const float sn = kBlkPerTile ? sa_row * sSB[sb_blk[nt]][kb - kb_begin] : s;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(part[r], s, acc[mt][nt][r]);
+        for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(part[r], sn, acc[mt][nt][r]);
       }
     }
   };
@@ -547,7 +556,7 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   // of the second: lane group g then holds columns 8 * (g / 2) .. + 7 of tile nt + (g & 1).
   const int col_s = n0 + wn * (TN / 4) + (g & 1) * 16 + (g >> 1) * 8;  // + nt * 16 (nt even)
 #pragma unroll
-  for (int nt = 0; nt < NT; nt += 2) {
+  for (int nt = 0; nt + 1 < NT; nt += 2) {
     f32x4 bx = {0.f, 0.f, 0.f, 0.f}, by = {0.f, 0.f, 0.f, 0.f};
     if (p.bias) {
       const int cx = min(col_w + nt * 16, p.n - 4), cy = min(col_w + nt * 16 + 16, p.n - 4);
@@ -568,6 +577,24 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
       const int row = row_w + mt * 16, col = col_s + nt * 16;
       if (row < p.m && col < p.n)
         *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + col) = v;
+    }
+  }
+  if constexpr (NT % 2 == 1) {
+    // the odd last column tile: each lane stores its 4 columns as 8 bytes
+    constexpr int nt = NT - 1;
+    const int col = col_w + nt * 16;
+    f32x4 bx = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias && col < p.n) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bx[r] = p.bias[col + r];
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const f32x4 x = acc[mt][nt] + bx;
+      const u32x2 v = {pack_out2(x[0], x[1], p.out_dtype), pack_out2(x[2], x[3], p.out_dtype)};
+      const int row = row_w + mt * 16;
+      if (row < p.m && col < p.n)
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + col) = v;
     }
   }
 }
@@ -595,9 +622,9 @@ static void finish_splits(Plan8& p, int64_t KB, int64_t s) {
   p.splits = (int)((KB + p.kb_per_split - 1) / p.kb_per_split);
 }
 
-// LDS plan for a given tile and split count. s = 0 picks it: 128x128 tiles split K into as many
-// parts as fill one 512-thread workgroup per CU (at most 4, >= 4 K blocks each); the larger tiles do
-// not split (measured: their partials, 2-4x larger, cost more than the parallelism gains).
+// LDS plan for a given tile and split count. s = 0 picks it: 128x128 and 128x192 tiles split K into
+// as many parts as fill one 512-thread workgroup per CU (at most 4, >= 4 K blocks each); the larger
+// tiles do not split (measured: their partials, 2-4x larger, cost more than the parallelism gains).
 static Plan8 plan8_lds(int64_t m, int64_t n, int64_t k, int tm, int tn, int64_t s = 0) {
   Plan8 p;
   p.kind = Kernel8::kLds;
@@ -608,7 +635,7 @@ static Plan8 plan8_lds(int64_t m, int64_t n, int64_t k, int tm, int tn, int64_t 
   const int64_t tiles = ((m + tm - 1) / tm) * ((n + tn - 1) / tn);
   p.grid_x = (int)tiles;
   if (s <= 0) {
-    s = tiles >= 256 || tm + tn > 256 ? 1 : 256 / tiles;
+    s = tiles >= 256 || tm + tn > 320 ? 1 : 256 / tiles;
     if (s > 4) s = 4;
     if (s > KB / 4) s = KB / 4;
   }
@@ -617,12 +644,14 @@ static Plan8 plan8_lds(int64_t m, int64_t n, int64_t k, int tm, int tn, int64_t 
 }
 
 // Estimated time (us) of an LDS plan, fitted to MI355X measurements over the DeepSeek-V3 shapes at
-// m = 128..8192 (it picks the fastest measured plan, or one within 2% of it, on all of them): per K
-// block of one tile (256x256: 1.96, 256x128 and 128x256: 1.15, 128x128: 0.70), rounds of 256
-// workgroups, a fixed 3 us per round, and for a K split the partial traffic (s * tile * 4 bytes,
-// stored and then summed by one workgroup at ~100 GB/s) plus 3 us.
+// m = 128..8192 (it picks the fastest measured plan, or one within 2% of it, on all of them; and the
+// fastest, or within 4%, of a sweep with the 192-column tiles at m = 1024..8192): per K block of one
+// tile (256x256: 1.96, 256x192: 1.55, 256x128 and 128x256: 1.15, 128x192: 0.90, 128x128: 0.70),
+// rounds of 256 workgroups, a fixed 3 us per round, and for a K split the partial traffic
+// (s * tile * 4 bytes, stored and then summed by one workgroup at ~100 GB/s) plus 3 us.
 static double lds_cost(const Plan8& p, int64_t k) {
-  const double step = p.tm + p.tn == 512 ? 1.96 : (p.tm + p.tn == 384 ? 1.15 : 0.70);
+  const int area = p.tm * p.tn;
+  const double step = area == 65536 ? 1.96 : area == 49152 ? 1.55 : area == 32768 ? 1.15 : area == 24576 ? 0.90 : 0.70;
   const int64_t wgs = (int64_t)p.grid_x * p.splits;
   const double rounds = (double)((wgs + 255) / 256);
   double t = rounds * (p.kb_per_split * step + 3.0);
@@ -632,11 +661,12 @@ static double lds_cost(const Plan8& p, int64_t k) {
 }
 
 static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
-  static const int kShapes[4][2] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}};
+  static const int kShapes[6][2] = {{256, 256}, {256, 192}, {256, 128}, {128, 256}, {128, 192}, {128, 128}};
   Plan8 best = plan8_lds(m, n, k, 128, 128);
   double best_t = lds_cost(best, k);
   for (const auto& sh : kShapes) {
     if (sh[0] > 128 && m <= 128) continue;  // half of every A tile would be padding
+    if (sh[1] == 192 && n % 192 != 0) continue;  // 192-column tiles only where they fit N exactly
     const Plan8 p = plan8_lds(m, n, k, sh[0], sh[1]);
     const double t = lds_cost(p, k);
     if (t < best_t) {
@@ -700,20 +730,26 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   else d.nt == 2 ? launch_stream<8, 2, FMT, PRE>(a, d, s) : launch_stream<8, 1, FMT, PRE>(a, d, s);
 }
 
-// Ring depth per tile shape: as many stages as 160 KiB of LDS holds.
+// Ring depth per tile shape: as many stages (at most 4) as 150 KiB of LDS holds.
 template <int TM, int TN, int FMT, bool PRE>
 static void launch_lds_t(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
-  constexpr int S = TM + TN == 512 ? 2 : (TM + TN == 384 ? 3 : 4);
+  constexpr int kStage = (TM + TN) * 128 + TM * 4;
+  constexpr int S = 150 * 1024 / kStage < 4 ? 150 * 1024 / kStage : 4;
   hipLaunchKernelGGL((gemm8_lds_kernel<TM, TN, S, FMT, PRE>), dim3((unsigned)(t.grid_x * t.splits)), dim3(512), 0, s,
                      a);
 }
 
 template <int FMT, bool PRE>
 static void launch_lds(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
-  if (t.tm == 256 && t.tn == 256) launch_lds_t<256, 256, FMT, PRE>(a, t, s);
-  else if (t.tm == 256) launch_lds_t<256, 128, FMT, PRE>(a, t, s);
-  else if (t.tn == 256) launch_lds_t<128, 256, FMT, PRE>(a, t, s);
-  else launch_lds_t<128, 128, FMT, PRE>(a, t, s);
+  if (t.tm == 256) {
+    if (t.tn == 256) launch_lds_t<256, 256, FMT, PRE>(a, t, s);
+    else if (t.tn == 192) launch_lds_t<256, 192, FMT, PRE>(a, t, s);
+    else launch_lds_t<256, 128, FMT, PRE>(a, t, s);
+  } else {
+    if (t.tn == 256) launch_lds_t<128, 256, FMT, PRE>(a, t, s);
+    else if (t.tn == 192) launch_lds_t<128, 192, FMT, PRE>(a, t, s);
+    else launch_lds_t<128, 128, FMT, PRE>(a, t, s);
+  }
 }
 
 }  // namespace aklr

@@ -152,6 +152,16 @@ def test_stream_shapes(m, n, k, bias):
     _run_and_check(m, n, k, variant="b_shuffled", bias=False, seed=52)
 
 
+# 192-column LDS tiles (planned where 192 divides N): ragged row tiles, bias and fp16 output on the odd
+# last column tile's 8-byte stores, b_scale blocks straddled by a wave's 48 columns (tiles start at
+# multiples of 64), 256- and 128-row tiles.
+@pytest.mark.parametrize("m,n,k,bias,fp16", [(2500, 2112, 1536, True, True), (4000, 2112, 512, True, False),
+                                             (4100, 4032, 1024, False, True)])
+def test_tile192_shapes(m, n, k, bias, fp16):
+    _run_and_check(m, n, k, mode="MN", bias=bias, out_dtype=torch.float16 if fp16 else None, seed=61)
+    _run_and_check(m, n, k, variant="b_shuffled", bias=False, seed=62)
+
+
 def test_out_buffer_and_determinism():
     m, n, k = 64, 7168, 16384
     q, s, b, bs = _fp8_inputs(m, n, k, seed=5)
