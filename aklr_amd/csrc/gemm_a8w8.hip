@@ -332,10 +332,11 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
 }
 
 // ---------------------------------------------------------------------------------------------
-// lds (m > 128): TM x TN workgroup tiles, 8 waves in 2 (m) x 4 (n), each wave (TM/2) x (TN/4), K steps
-// of 128 through an S-stage LDS ring that S - 1 stages fill ahead of the compute. A, B and a_scale go
-// global -> LDS with direct-to-LDS buffer loads (no register staging), every wave issuing the same
-// number of loads per stage, so one immediate wait count leaves exactly S - 2 stages in flight.
+// lds (m > 128): TM x TN workgroup tiles, 8 waves in 2 (m) x 4 (n) -- 4 x 2 for TN = 224 -- each wave
+// (TM/WM) x (TN/WN), K steps of 128 through an S-stage LDS ring that S - 1 stages fill ahead of the
+// compute. A, B and a_scale go global -> LDS with direct-to-LDS buffer loads (no register staging),
+// every wave issuing the same number of loads per stage, so one immediate wait count leaves exactly
+// S - 2 stages in flight.
 // Each LDS operand tile is rows of 128 bytes with the 16-byte chunks XOR-swizzled by row (chunk c of
 // row r at position c ^ (r & 7)): lane i of a load writes position i % 8 of row i / 8 of its 8-row
 // slab and so fetches chunk (i % 8) ^ (r & 7) of that row; the MFMA fragment reads (row li, chunks
@@ -349,15 +350,23 @@ constexpr int kLdsGroup = 8;  // tile rows per raster group
 
 template <int TM, int TN, int S, int FMT, bool PRE>
 __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
-  static_assert(TM % 64 == 0 && (TN == 128 || TN == 192 || TN == 256) && S >= 2, "tile shape");
-  constexpr int MT = TM / 32, NT = TN / 64;  // 16x16 tiles per wave along m and n
-  // TN = 192 (for N = 2112 = 11 x 192): tiles start at multiples of 64 columns, so a wave's 48 columns
-  // can straddle two 128-column b_scale blocks, and its b_scale is taken per column tile.
+  static_assert(TM % 64 == 0 && (TN == 128 || TN == 192 || TN == 224 || TN == 256) && S >= 2, "tile shape");
+  constexpr int WN = TN == 224 ? 2 : 4, WM = 8 / WN;  // waves along n and m
+  constexpr int MT = TM / (16 * WM), NT = TN / (16 * WN);  // 16x16 tiles per wave along m and n
+  // TN = 192 (N = 2112 = 11 x 192) and 224 (N = 7168 = 32 x 224): tiles start at multiples of 64 or
+  // 32 columns, so a wave's columns can straddle 128-column b_scale blocks, and its b_scale is taken
+  // per column tile.
   constexpr bool kBlkPerTile = TN % 128 != 0;
-  constexpr int kNBlk = (TN + 127) / 128;  // 128-column b_scale blocks a tile spans (n0 % 128 is 0 or 64)
-  constexpr int AI = TM / 64, BI = TN / 64;  // 1 KiB loads per wave per stage
+  constexpr int kNBlk = TN == 224 ? 3 : (TN + 127) / 128;  // 128-column b_scale blocks a tile spans
+  // B moves in slabs of 8 rows, BI per wave. When the slabs do not divide evenly (TN = 224: 28 slabs),
+  // wave w takes slabs w, w + 8, ... and the slots past TN issue an empty load into the stage's spare
+  // rows, so every wave's count stays the same.
+  constexpr int kSlabsB = TN / 8;
+  constexpr int BI = (kSlabsB + 7) / 8;
+  constexpr bool kEvenB = kSlabsB % 8 == 0;
+  constexpr int AI = TM / 64;                // 1 KiB A loads per wave per stage
   constexpr int kLoads = AI + BI + 1;        // + one a_scale load
-  constexpr int kStageA = TM * 128, kStageB = TN * 128;
+  constexpr int kStageA = TM * 128, kStageB = BI * 8 * 1024;
   constexpr int kScaleWaves = TM / 64;       // waves whose a_scale load carries rows
   __shared__ __attribute__((aligned(1024))) uint8_t sA[S * kStageA];
   __shared__ __attribute__((aligned(1024))) uint8_t sB[S * kStageB];
@@ -382,15 +391,15 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 15, g = lane >> 4;
-  const int wm = w >> 2, wn = w & 3;
+  const int wm = w / WN, wn = w % WN;
   const int KB = p.k >> 7;
   const int kb_begin = split * p.kb_per_split;
   const int kb_end = min(KB, kb_begin + p.kb_per_split);
   const int64_t kt32 = p.k >> 5;
 
-  // Wave w moves rows [w*TM/8, (w+1)*TM/8) of the A tile and [w*TN/8, (w+1)*TN/8) of the B tile in
-  // slabs of 8 rows; waves below kScaleWaves move a_scale rows [64w, 64w + 64), the others issue an
-  // empty load so that every wave's count per stage is kLoads.
+  // Wave w moves rows [w*TM/8, (w+1)*TM/8) of the A tile and its BI slabs of the B tile, in slabs of 8
+  // rows; waves below kScaleWaves move a_scale rows [64w, 64w + 64), the others issue an empty load so
+  // that every wave's count per stage is kLoads.
   const i32x4 ars = make_rsrc_words(p.a + (int64_t)m0 * p.lda, rsrc_bytes((int64_t)(p.m - 1 - m0) * p.lda + p.k));
   const int64_t b_base = PRE ? (int64_t)(n0 >> 4) * kt32 * 512 : (int64_t)n0 * p.ldb;
   const int64_t b_total = PRE ? (int64_t)p.n * p.k : (int64_t)(p.n - 1) * p.ldb + p.k;
@@ -408,8 +417,11 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   }
 #pragma unroll
   for (int j = 0; j < BI; ++j) {
-    const int r = w * (TN / 8) + j * 8 + lr;
-    if (PRE)
+    const int slab = kEvenB ? w * BI + j : w + 8 * j;
+    const int r = slab * 8 + lr;
+    if (slab >= kSlabsB)
+      b_off[j] = kOobOffset;
+    else if (PRE)
       b_off[j] = n0 + r < p.n ? (uint32_t)((((r >> 4) * kt32 + (c >> 1)) * 512) + (c & 1) * 256 + (r & 15) * 16)
                               : kOobOffset;
     else
@@ -418,7 +430,9 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   const bool scale_wave = w < kScaleWaves;
   const uint32_t sa_off =
       scale_wave && m0 + w * 64 + lane < p.m ? (uint32_t)((w * 64 + lane) * p.sa_sm * 4) : kOobOffset;
-  const uint32_t lds_a = lds_addr(&sA[w * (TM / 8) * 128]), lds_b = lds_addr(&sB[w * (TN / 8) * 128]);
+  const uint32_t lds_a = lds_addr(&sA[w * (TM / 8) * 128]);
+  const uint32_t lds_b = lds_addr(&sB[(kEvenB ? w * BI : w) * 1024]);
+  constexpr uint32_t kSlabStrideB = kEvenB ? 1024 : 8 * 1024;  // LDS bytes between a wave's B slabs
   const uint32_t lds_s = scale_wave ? lds_addr(&sS[w * 64]) : lds_addr(&sDummy[w * 64]);
   const uint32_t lds_s_step = scale_wave ? TM * 4 : 0;
   auto issue = [&](int kb, int st) {
@@ -427,7 +441,8 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
 #pragma unroll
     for (int j = 0; j < AI; ++j) lds_dma16(ars, lds_a + st * kStageA + j * 1024, on ? a_off[j] + ak : kOobOffset);
 #pragma unroll
-    for (int j = 0; j < BI; ++j) lds_dma16(brs, lds_b + st * kStageB + j * 1024, on ? b_off[j] + bk : kOobOffset);
+    for (int j = 0; j < BI; ++j)
+      lds_dma16(brs, lds_b + st * kStageB + j * kSlabStrideB, on && b_off[j] != kOobOffset ? b_off[j] + bk : kOobOffset);
     lds_dma4(sars, lds_s + st * lds_s_step,
              on && sa_off != kOobOffset ? sa_off + (uint32_t)(kb * p.sa_sk * 4) : kOobOffset);
   };
@@ -448,16 +463,16 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
       sSB[r][kk] = p.sb[(int64_t)min((n0 >> 7) + r, last_row) * p.ldbs + kb_begin + kk];
     }
   }
-  const float* sbw = sSB[((n0 + wn * (TN / 4)) >> 7) - (n0 >> 7)];
+  const float* sbw = sSB[((n0 + wn * (TN / WN)) >> 7) - (n0 >> 7)];
   int sb_blk[NT];  // kBlkPerTile: each column tile's block
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) sb_blk[nt] = ((n0 + wn * (TN / 4) + nt * 16) >> 7) - (n0 >> 7);
+  for (int nt = 0; nt < NT; ++nt) sb_blk[nt] = ((n0 + wn * (TN / WN) + nt * 16) >> 7) - (n0 >> 7);
 
   // Fragment addresses: every row a lane reads is congruent to li mod 8, so the swizzle term is the
   // same for all its row tiles and each read is one base plus an immediate (tile * 2048 bytes).
   const int swz_lo = (g ^ (li & 7)) << 4, swz_hi = ((4 + g) ^ (li & 7)) << 4;
-  const int a_row = (wm * (TM / 2) + li) * 128, b_row = (wn * (TN / 4) + li) * 128;
-  const int s_row = wm * (TM / 2) + li;
+  const int a_row = (wm * (TM / WM) + li) * 128, b_row = (wn * (TN / WN) + li) * 128;
+  const int s_row = wm * (TM / WM) + li;
   auto compute = [&](int kb, int st) {
     const float sb = sbw[kb - kb_begin];
     const uint8_t* A = sA + st * kStageA;
@@ -503,8 +518,8 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  const int row_w = m0 + wm * (TM / 2) + li;  // + mt * 16: the lane's output row
-  const int col_w = n0 + wn * (TN / 4) + 4 * g;  // + nt * 16: the lane's first output column
+  const int row_w = m0 + wm * (TM / WM) + li;  // + mt * 16: the lane's output row
+  const int col_w = n0 + wn * (TN / WN) + 4 * g;  // + nt * 16: the lane's first output column
   if (p.splits > 1) {
     // partials in accumulator order, [split][tile][wave][mt][nt][lane] x 4 fp32: the workgroup that
     // reduces them runs the same lanes over the same tiles, so every store and load is 1 KiB of
@@ -554,7 +569,7 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   // Output: for each pair of column tiles (nt, nt + 1) a lane packs its 4 columns of each into two
   // words, and permlane16_swap exchanges the odd lane groups of the first with the even lane groups
   // of the second: lane group g then holds columns 8 * (g / 2) .. + 7 of tile nt + (g & 1).
-  const int col_s = n0 + wn * (TN / 4) + (g & 1) * 16 + (g >> 1) * 8;  // + nt * 16 (nt even)
+  const int col_s = n0 + wn * (TN / WN) + (g & 1) * 16 + (g >> 1) * 8;  // + nt * 16 (nt even)
 #pragma unroll
   for (int nt = 0; nt + 1 < NT; nt += 2) {
     f32x4 bx = {0.f, 0.f, 0.f, 0.f}, by = {0.f, 0.f, 0.f, 0.f};
@@ -645,13 +660,18 @@ static Plan8 plan8_lds(int64_t m, int64_t n, int64_t k, int tm, int tn, int64_t 
 
 // Estimated time (us) of an LDS plan, fitted to MI355X measurements over the DeepSeek-V3 shapes at
 // m = 128..8192 (it picks the fastest measured plan, or one within 2% of it, on all of them; and the
-// fastest, or within 4%, of a sweep with the 192-column tiles at m = 1024..8192): per K block of one
-// tile (256x256: 1.96, 256x192: 1.55, 256x128 and 128x256: 1.15, 128x192: 0.90, 128x128: 0.70),
-// rounds of 256 workgroups, a fixed 3 us per round, and for a K split the partial traffic
-// (s * tile * 4 bytes, stored and then summed by one workgroup at ~100 GB/s) plus 3 us.
+// fastest, or within 4%, of sweeps with the 192- and 224-column tiles at m = 1024..8192): per K block
+// of one tile (256x256: 1.96, 256x224: 1.76, 256x192: 1.55, 256x128 and 128x256: 1.15, 128x192: 0.90,
+// 128x128: 0.70), rounds of 256 workgroups, a fixed 3 us per round, and for a K split the partial
+// traffic (s * tile * 4 bytes, stored and then summed by one workgroup at ~100 GB/s) plus 3 us.
 static double lds_cost(const Plan8& p, int64_t k) {
   const int area = p.tm * p.tn;
-  const double step = area == 65536 ? 1.96 : area == 49152 ? 1.55 : area == 32768 ? 1.15 : area == 24576 ? 0.90 : 0.70;
+  const double step = area == 65536   ? 1.96
+                      : area == 57344 ? 1.76
+                      : area == 49152 ? 1.55
+                      : area == 32768 ? 1.15
+                      : area == 24576 ? 0.90
+                                      : 0.70;
   const int64_t wgs = (int64_t)p.grid_x * p.splits;
   const double rounds = (double)((wgs + 255) / 256);
   double t = rounds * (p.kb_per_split * step + 3.0);
@@ -661,12 +681,13 @@ static double lds_cost(const Plan8& p, int64_t k) {
 }
 
 static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
-  static const int kShapes[6][2] = {{256, 256}, {256, 192}, {256, 128}, {128, 256}, {128, 192}, {128, 128}};
+  static const int kShapes[7][2] = {{256, 256}, {256, 224}, {256, 192}, {256, 128},
+                                    {128, 256}, {128, 192}, {128, 128}};
   Plan8 best = plan8_lds(m, n, k, 128, 128);
   double best_t = lds_cost(best, k);
   for (const auto& sh : kShapes) {
     if (sh[0] > 128 && m <= 128) continue;  // half of every A tile would be padding
-    if (sh[1] == 192 && n % 192 != 0) continue;  // 192-column tiles only where they fit N exactly
+    if ((sh[1] == 192 || sh[1] == 224) && n % sh[1] != 0) continue;  // only where they fit N exactly
     const Plan8 p = plan8_lds(m, n, k, sh[0], sh[1]);
     const double t = lds_cost(p, k);
     if (t < best_t) {
@@ -733,7 +754,7 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
 // Ring depth per tile shape: as many stages (at most 4) as 150 KiB of LDS holds.
 template <int TM, int TN, int FMT, bool PRE>
 static void launch_lds_t(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
-  constexpr int kStage = (TM + TN) * 128 + TM * 4;
+  constexpr int kStage = (TM + (TN / 8 + 7) / 8 * 64) * 128 + TM * 4;
   constexpr int S = 150 * 1024 / kStage < 4 ? 150 * 1024 / kStage : 4;
   hipLaunchKernelGGL((gemm8_lds_kernel<TM, TN, S, FMT, PRE>), dim3((unsigned)(t.grid_x * t.splits)), dim3(512), 0, s,
                      a);
@@ -743,6 +764,7 @@ template <int FMT, bool PRE>
 static void launch_lds(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
   if (t.tm == 256) {
     if (t.tn == 256) launch_lds_t<256, 256, FMT, PRE>(a, t, s);
+    else if (t.tn == 224) launch_lds_t<256, 224, FMT, PRE>(a, t, s);
     else if (t.tn == 192) launch_lds_t<256, 192, FMT, PRE>(a, t, s);
     else launch_lds_t<256, 128, FMT, PRE>(a, t, s);
   } else {

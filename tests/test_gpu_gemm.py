@@ -152,12 +152,14 @@ def test_stream_shapes(m, n, k, bias):
     _run_and_check(m, n, k, variant="b_shuffled", bias=False, seed=52)
 
 
-# 192-column LDS tiles (planned where 192 divides N): ragged row tiles, bias and fp16 output on the odd
-# last column tile's 8-byte stores, b_scale blocks straddled by a wave's 48 columns (tiles start at
-# multiples of 64), 256- and 128-row tiles.
+# 192- and 224-column LDS tiles (planned where they divide N): ragged row tiles, bias and fp16 output on
+# the odd last column tile's 8-byte stores, b_scale blocks straddled by a wave's columns (tiles start at
+# multiples of 64 or 32 columns), 256- and 128-row tiles, the 4 x 2 wave layout and the uneven B slabs
+# of the 224-column tile.
 @pytest.mark.parametrize("m,n,k,bias,fp16", [(2500, 2112, 1536, True, True), (4000, 2112, 512, True, False),
-                                             (4100, 4032, 1024, False, True)])
-def test_tile192_shapes(m, n, k, bias, fp16):
+                                             (4100, 4032, 1024, False, True), (2000, 7168, 2048, True, True),
+                                             (3000, 4480, 1024, False, False)])
+def test_192_224_column_tiles(m, n, k, bias, fp16):
     _run_and_check(m, n, k, mode="MN", bias=bias, out_dtype=torch.float16 if fp16 else None, seed=61)
     _run_and_check(m, n, k, variant="b_shuffled", bias=False, seed=62)
 
