@@ -6,7 +6,7 @@ outputs or a ``FallbackReason``. They run hand-written HIP kernels through the C
 ``include/aklr_amd.h`` (``libaklr_amd.so``, built in-tree by ``aklr_amd._build``).
 """
 from .dispatch import FallbackReason, KernelInfo
-from .gemm import gemm_a4w4_mxfp4, gemm_a8w8_blockwise_scaled
+from .gemm import gemm_a4w4_mxfp4, gemm_a8w8_blockwise_scaled, quant_gemm_a8w8_blockwise_scaled
 from .moe import deepseek_v2_fp8_moe, moe_fp8_experts, moe_fp8_route
 from .quant import dynamic_mxfp4_quant, per_group_quant_fp8, per_group_quant_mxfp8
 
@@ -21,4 +21,5 @@ __all__ = [
     "moe_fp8_route",
     "per_group_quant_fp8",
     "per_group_quant_mxfp8",
+    "quant_gemm_a8w8_blockwise_scaled",
 ]

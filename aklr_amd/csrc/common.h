@@ -92,6 +92,12 @@ __device__ __forceinline__ void stage_barrier() {
 constexpr float kInv448 = 0x1.24924ap-9f;
 constexpr float kAmaxFloor = 1e-10f;
 
+// v read from another lane of the same 16-lane row through a DPP control (quad_perm, row_mirror, ...).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 

@@ -59,8 +59,20 @@ struct StreamFrag {
   i32x8 b[NT];
 };
 
-template <int MT, int NT, int NW, int D, int NS, int FMT, bool PRE>
+// Fused activation quantization (QA, MT <= 4): p.a is then bf16 x [m, lda elements], and the compute
+// waves quantize each K block of it per 1 x 128 group with the arithmetic of quant_fp8_1x128_kernel
+// (amax floored at 1e-10, s = amax * fl(1/448), codes e4m3(clamp(x * (1/s)))), writing the codes in
+// fragment order and s into the stage: the LDS stage holds exactly the bytes the loader would have
+// moved from per_group_quant_fp8's output. Compute wave w quantizes rows [4 MT w, 4 MT (w + 1)) of
+// the MT * 16: 16 / MT lanes per row, 8 MT values (MT 16-byte loads) per lane.
+template <int MT>
+struct XStage {
+  u32x4 v[MT];
+};
+
+template <int MT, int NT, int NW, int D, int NS, int FMT, bool PRE, bool QA = false>
 __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p) {
+  static_assert(!QA || (MT == 1 && FMT == 0 && NW == 4), "fused quantization: e4m3, one row tile, 4 waves");
   static_assert(NS >= 2 && D >= 1 && MT >= 1 && MT <= 8 && 128 % (NT * 16) == 0, "stream shape");
   constexpr int kSRows = (MT * 16 + 63) / 64 * 64;  // a_scale floats per stage: whole 64-lane loads
   constexpr int kLoadsA = 2 * MT + kSRows / 64;     // loader loads per stage
@@ -70,6 +82,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   __shared__ __attribute__((aligned(1024))) uint8_t sA[NS][MT * 2048];
   __shared__ __attribute__((aligned(16))) float sS[NS][kSRows];
   __shared__ float sSB[kNBlk][512];
+  __shared__ float sQSink[QA ? 64 : 1];  // fused quantization: landing place of the unused scale stores
   __shared__ unsigned arrive_slot;
 
   const int lane = threadIdx.x & 63;
@@ -93,7 +106,18 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   const int64_t stream_plane = (int64_t)gridDim.x * NW * MT * NT * 256;
   const int64_t part_base = ((int64_t)blockIdx.x * NW + w) * (MT * NT) * 256 + lane * 4;
 
-  if (w == NW) {
+  if (QA && w == NW) {
+    // Fused quantization: the compute waves fill the A stages; the loader stages b_scale and keeps
+    // the barrier count.
+    const int len = kb_end - kb_begin;
+    const int last_row = (p.n - 1) >> 7;
+    for (int i = lane; i < kNBlk * len; i += 64) {
+      const int r = i / len, kk = i - r * len;
+      sSB[r][kk] = p.sb[(int64_t)min((n0 >> 7) + r, last_row) * p.ldbs + kb_begin + kk];
+    }
+    stage_barrier();
+    for (int kb = kb_begin; kb < kb_end; ++kb) stage_barrier();
+  } else if (w == NW) {
     // Loader. Rows past m read the out-of-range offset: zeros, no memory access.
     const i32x4 ars = make_rsrc_words(p.a, rsrc_bytes((int64_t)(p.m - 1) * p.lda + p.k));
     const i32x4 sars =
@@ -172,6 +196,73 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     };
     const float* sbw = sSB[(c0w >> 7) - (n0 >> 7)];
 
+    // Fused quantization: this wave's rows of each stage (see XStage), from an x register ring that runs
+    // beside the weight ring.
+    constexpr int kLpr = 16 / MT;  // lanes per row
+    const int qrow = w * 4 * MT + lane / kLpr, qp = lane % kLpr;
+    const rsrc_t xrs = make_rsrc(p.a, QA ? rsrc_bytes(((int64_t)(p.m - 1) * p.lda + p.k) * 2) : 0u);
+    const uint32_t x_off = QA && qrow < p.m ? (uint32_t)(((int64_t)qrow * p.lda + qp * 8 * MT) * 2) : kOobOffset;
+    auto xload = [&](int kb, XStage<MT>& xs) {
+      const bool on = kb < kb_end && x_off != kOobOffset;
+#pragma unroll
+      for (int i = 0; i < MT; ++i) xs.v[i] = buf_ld16(xrs, on ? x_off + (uint32_t)kb * 256u + 16u * i : kOobOffset);
+    };
+    auto qwrite = [&](const XStage<MT>& xs, int slot) {
+      float f[8 * MT];
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const uint32_t wv[4] = {xs.v[i].x, xs.v[i].y, xs.v[i].z, xs.v[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          f[8 * i + 2 * j] = bf16_lo(wv[j]);
+          f[8 * i + 2 * j + 1] = bf16_hi(wv[j]);
+        }
+      }
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8 * MT; ++i) amax = fmaxf(amax, fabsf(f[i]));
+      // a row's lanes are one quad, half row or row of 16 lanes: reduce with DPP moves, not LDS permutes
+      amax = fmaxf(amax, dpp_f32<0xB1>(amax));                   // quad_perm [1,0,3,2]
+      amax = fmaxf(amax, dpp_f32<0x4E>(amax));                   // quad_perm [2,3,0,1]
+      if constexpr (kLpr >= 8) amax = fmaxf(amax, dpp_f32<0x141>(amax));  // row_half_mirror
+      if constexpr (kLpr >= 16) amax = fmaxf(amax, dpp_f32<0x140>(amax));  // row_mirror
+      amax = fmaxf(amax, kAmaxFloor);
+      const float sc = amax * kInv448;  // rounds once to fp32
+      const float inv = 1.0f / sc;      // IEEE division, as the quantizer
+      uint32_t o[2 * MT];
+#pragma unroll
+      for (int i = 0; i < 2 * MT; ++i) {
+        const float a = fminf(fmaxf(f[4 * i + 0] * inv, -448.0f), 448.0f);
+        const float b = fminf(fmaxf(f[4 * i + 1] * inv, -448.0f), 448.0f);
+        const float c = fminf(fmaxf(f[4 * i + 2] * inv, -448.0f), 448.0f);
+        const float d = fminf(fmaxf(f[4 * i + 3] * inv, -448.0f), 448.0f);
+        o[i] = pack4_e4m3(a, b, c, d);
+      }
+      // byte b0 of the row lands in chunk (row tile, b0 / 64), lane group (b0 % 64) / 16
+      const int b0 = qp * 8 * MT;
+      uint8_t* dst = &sA[slot][(qrow >> 4) * 2048 + (b0 >> 6) * 1024 + ((((b0 & 63) >> 4) * 16) + (qrow & 15)) * 16 +
+                               (b0 & 15)];
+      if constexpr (MT == 1) {
+        *reinterpret_cast<u32x2*>(dst) = u32x2{o[0], o[1]};
+      } else {
+        *reinterpret_cast<u32x4*>(dst) = u32x4{o[0], o[1], o[2], o[3]};
+        if constexpr (MT == 4) *reinterpret_cast<u32x4*>(dst + 256) = u32x4{o[4], o[5], o[6], o[7]};
+      }
+      // one lane per row stores the scale, the others store into sQSink: a branch here would split the
+      // step into blocks and let the compiler sink the step's MFMAs past the following barriers
+      *(qp == 0 ? &sS[slot][qrow] : &sQSink[lane]) = sc;
+    };
+    XStage<MT> xr[QA ? D : 1];
+    if constexpr (QA) {
+      // every slot starts filled: stages kb_begin .. kb_begin + NS - 1, loaded together
+      XStage<MT> pro[NS];
+#pragma unroll
+      for (int s0 = 0; s0 < NS; ++s0) xload(kb_begin + s0, pro[s0]);
+#pragma unroll
+      for (int s0 = 0; s0 < NS; ++s0) qwrite(pro[s0], s0);
+    }
+    int qs = 0;  // QA: slot of stage kb during block kb, which takes stage kb + NS
+
     // Fragments are read one K block ahead: the MFMAs of block kb run on registers read during block
     // kb - 1, and each row tile's registers take block kb + 1's fragment as soon as its MFMAs have
     // issued, so the LDS latency hides behind the MFMAs instead of stalling them. Then the weight slot
@@ -187,9 +278,17 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) read_frags(mt, 0);
     int st = 0;  // slot of stage kb + 1 during block kb
-    auto step = [&](int kb, StreamFrag<NT>& f) {
+    auto step = [&](int kb, StreamFrag<NT>& f, XStage<MT>& xq) {
       stage_barrier();  // publishes stage kb + 1; every wave is done reading stage kb
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (QA) {
+        // Stage kb + NS into the slot stage kb leaves. Its x arrived before this block's weights (the x
+        // loads of a block are issued ahead of its weight loads), so this work fills the wait for them.
+        qwrite(xq, qs);
+        xload(kb + NS + D, xq);
+        qs = qs + 1 == NS ? 0 : qs + 1;
+        __builtin_amdgcn_sched_barrier(0);
+      }
       st = st + 1 == NS ? 0 : st + 1;
       const float sb = sbw[kb - kb_begin];
 #pragma unroll
@@ -219,17 +318,23 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     // D-deep ring: block kb_begin + i lives in slot i % D. Whole groups of D blocks run in a loop with
     // no exit inside (its head then has one ring state, and the compiler waits for exactly the slot
     // it consumes); the remaining < D blocks follow, one guarded step each.
+    // The x ring's loads go out just ahead of the weight loads of the same slot, in the order the steps
+    // issue them, so that the loop head sees one order of outstanding loads and waits for no more
+    // than the slot it consumes.
     StreamFrag<NT> f[D];
 #pragma unroll
-    for (int j = 0; j < D; ++j) load(kb_begin + j, f[j]);
+    for (int j = 0; j < D; ++j) {
+      if constexpr (QA) xload(kb_begin + NS + j, xr[j]);
+      load(kb_begin + j, f[j]);
+    }
     const int len = kb_end - kb_begin, full = len / D * D;
     for (int kb0 = kb_begin; kb0 < kb_begin + full; kb0 += D) {
 #pragma unroll
-      for (int j = 0; j < D; ++j) step(kb0 + j, f[j]);
+      for (int j = 0; j < D; ++j) step(kb0 + j, f[j], xr[QA ? j : 0]);
     }
 #pragma unroll
     for (int j = 0; j < D - 1; ++j)
-      if (full + j < len) step(kb_begin + full + j, f[j]);
+      if (full + j < len) step(kb_begin + full + j, f[j], xr[QA ? j : 0]);
     if (p.splits > 1) {
       // partials in accumulator order, [split][group][wave][tile][lane] x 4 fp32: the workgroup that
       // reduces them runs the same lanes over the same tiles, so every store and load is 1 KiB of
@@ -736,11 +841,11 @@ static size_t workspace8(const Plan8& p) {
 }
 
 // Stream kernel: 4 compute waves and 4 A stages; ring depth 4 at 1-2 row tiles, else 2 (measured).
-template <int MT, int NT, int FMT, bool PRE>
+template <int MT, int NT, int FMT, bool PRE, bool QA = false>
 static void launch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   constexpr int D = MT <= 2 ? 4 : 2;
-  hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, 4, D, 4, FMT, PRE>), dim3((unsigned)d.grid_x, (unsigned)d.splits),
-                     dim3(5 * 64), 0, s, a);
+  hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, 4, D, 4, FMT, PRE, QA>),
+                     dim3((unsigned)d.grid_x, (unsigned)d.splits), dim3(5 * 64), 0, s, a);
 }
 
 template <int FMT, bool PRE>
@@ -749,6 +854,31 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   else if (d.mt == 2) d.nt == 2 ? launch_stream<2, 2, FMT, PRE>(a, d, s) : launch_stream<2, 1, FMT, PRE>(a, d, s);
   else if (d.mt == 4) d.nt == 2 ? launch_stream<4, 2, FMT, PRE>(a, d, s) : launch_stream<4, 1, FMT, PRE>(a, d, s);
   else d.nt == 2 ? launch_stream<8, 2, FMT, PRE>(a, d, s) : launch_stream<8, 1, FMT, PRE>(a, d, s);
+}
+
+// The fused-quantization stream kernel serves plans of one row tile (m <= 16); larger m quantizes into
+// the workspace and runs the GEMM. Measured on the DeepSeek-V3 shapes: one row tile saves 1-1.5 us a
+// call over the two launches; at 2 row tiles (8 values a lane) the two are even, at 4 (32 values a
+// lane) the quantization outgrows the wait for the weights and the fused call is 15-25% slower.
+static bool fused_quant_ok(const Plan8& p) { return p.kind == Kernel8::kStream && p.mt == 1; }
+
+template <bool PRE>
+static void dispatch_stream_qa(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
+  d.nt == 2 ? launch_stream<1, 2, 0, PRE, true>(a, d, s) : launch_stream<1, 1, 0, PRE, true>(a, d, s);
+}
+
+// Workspace of the fused entry point: the GEMM's split-K workspace, then (unfused plans) the codes
+// [m, k] and group-major scales [k/128, m] of the quantized activations, each 256-byte aligned. The
+// codes start past the counter region even when the GEMM runs unsplit: a workspace is shared by
+// calls whose counters must stay zero.
+static size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
+static size_t quant_codes_offset(const Plan8& p) {
+  const size_t gemm = up256(workspace8(p));
+  return gemm > kSplitkCounterBytes ? gemm : kSplitkCounterBytes;
+}
+static size_t quant_gemm_workspace(const Plan8& p, int64_t m, int64_t k) {
+  if (fused_quant_ok(p)) return workspace8(p);
+  return quant_codes_offset(p) + up256((size_t)m * k) + up256((size_t)(k / 128) * m * 4);
 }
 
 // Ring depth per tile shape: as many stages (at most 4) as 150 KiB of LDS holds.
@@ -845,6 +975,75 @@ extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void*
     if (e5) pre ? launch_lds<1, true>(g, plan, stream) : launch_lds<1, false>(g, plan, stream);
     else pre ? launch_lds<0, true>(g, plan, stream) : launch_lds<0, false>(g, plan, stream);
   }
+  AKLR_LAUNCH_CHECK();
+  return AKLR_OK;
+}
+
+extern "C" size_t aklr_quant_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k < 128) return 0;
+  return quant_gemm_workspace(plan8(m, n, k), m, k);
+}
+
+extern "C" int aklr_quant_gemm_a8w8_blockscale(const void* x, int64_t ldx, const void* b, int64_t ldb,
+                                               const float* b_scale, int64_t ldbs, const float* bias, void* out,
+                                               int64_t ldo, int64_t m, int64_t n, int64_t k, int b_layout,
+                                               int out_dtype, void* workspace, size_t workspace_bytes,
+                                               hipStream_t stream) {
+  if (!x || !b || !b_scale || !out) return AKLR_ERR_INVALID_ARGUMENT;
+  if (m < 0 || n <= 0 || k <= 0 || k % 128 != 0 || n % 16 != 0) return AKLR_ERR_INVALID_ARGUMENT;
+  if (m > (1 << 20) || n > 262144 || k > 65536) return AKLR_ERR_INVALID_ARGUMENT;
+  if (b_layout != AKLR_B_ROW_MAJOR && b_layout != AKLR_B_PRESHUFFLE_16x16) return AKLR_ERR_UNSUPPORTED;
+  if (out_dtype != AKLR_OUT_BF16 && out_dtype != AKLR_OUT_F16) return AKLR_ERR_UNSUPPORTED;
+  if (!aklr_aligned16(x) || !aklr_aligned16(b) || !aklr_aligned16(out)) return AKLR_ERR_INVALID_ARGUMENT;
+  if ((reinterpret_cast<uintptr_t>(b_scale) & 3u) || (bias && (reinterpret_cast<uintptr_t>(bias) & 3u)))
+    return AKLR_ERR_INVALID_ARGUMENT;
+  if (ldx < k || ldx % 8 != 0 || ldo < n || ldo % 8 != 0) return AKLR_ERR_INVALID_ARGUMENT;
+  if (b_layout == AKLR_B_ROW_MAJOR && (ldb < k || ldb % 16 != 0 || ldb >= (1 << 23))) return AKLR_ERR_INVALID_ARGUMENT;
+  if (ldbs < k / 128) return AKLR_ERR_INVALID_ARGUMENT;
+  if (m == 0) return AKLR_OK;
+  const Plan8 plan = plan8(m, n, k);
+  const size_t need = quant_gemm_workspace(plan, m, k);
+  if (need > 0 && (!workspace || workspace_bytes < need || !aklr_aligned16(workspace))) return AKLR_ERR_WORKSPACE;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+
+  if (!fused_quant_ok(plan)) {
+    // quantize into the workspace (past the GEMM's part), then the GEMM reads it
+    uint8_t* q = ws + quant_codes_offset(plan);
+    float* sc = reinterpret_cast<float*>(q + up256((size_t)m * k));
+    int st = aklr_per_group_quant_fp8(x, ldx, q, sc, m, k, stream);
+    if (st != AKLR_OK) return st;
+    return aklr_gemm_a8w8_blockscale(q, k, b, ldb, sc, 1, m, b_scale, ldbs, bias, out, ldo, m, n, k,
+                                     AKLR_FP8_E4M3FN, b_layout, out_dtype, workspace8(plan) ? ws : nullptr,
+                                     workspace8(plan), stream);
+  }
+  // the loader addresses x with 32-bit byte offsets from its first row
+  if (((m - 1) * ldx + k) * 2 > 0x7FFFFFFFll) return AKLR_ERR_INVALID_ARGUMENT;
+  Gemm8Args g;
+  g.a = static_cast<const uint8_t*>(x);
+  g.lda = ldx;
+  g.b = static_cast<const uint8_t*>(b);
+  g.ldb = ldb;
+  g.sa = nullptr;  // the loader computes the scales
+  g.sa_sm = g.sa_sk = 0;
+  g.sb = b_scale;
+  g.ldbs = ldbs;
+  g.bias = bias;
+  g.out = out;
+  g.ldo = ldo;
+  g.m = (int)m;
+  g.n = (int)n;
+  g.k = (int)k;
+  g.out_dtype = out_dtype;
+  g.counters = nullptr;
+  g.partial = nullptr;
+  g.splits = plan.splits;
+  g.kb_per_split = plan.kb_per_split;
+  if (plan.splits > 1) {
+    g.counters = reinterpret_cast<unsigned*>(ws);
+    g.partial = reinterpret_cast<float*>(ws + kSplitkCounterBytes);
+  }
+  if (b_layout == AKLR_B_PRESHUFFLE_16x16) dispatch_stream_qa<true>(g, plan, stream);
+  else dispatch_stream_qa<false>(g, plan, stream);
   AKLR_LAUNCH_CHECK();
   return AKLR_OK;
 }

@@ -192,6 +192,89 @@ def gemm_a8w8_blockwise_scaled(
 
 # ---------------------------------------------------------------------------------------------
 @dataclass
+class _QuantGemm8Plan:
+    x: torch.Tensor
+    b: torch.Tensor
+    b_scale: torch.Tensor
+    bias: torch.Tensor | None
+    out: torch.Tensor | None
+    out_dtype: torch.dtype
+    m: int
+    n: int
+    k: int
+    b_layout: int
+    variant: str
+    kernel_ref: str = field(default="")
+
+
+def _run_quant_gemm8(p: _QuantGemm8Plan):
+    dev = p.x.device
+    out = p.out if p.out is not None else torch.empty((p.m, p.n), dtype=p.out_dtype, device=dev)
+    L = _lib.lib()
+    ws_bytes = L.aklr_quant_gemm_a8w8_blockscale_workspace_bytes(p.m, p.n, p.k)
+    ws = workspace.get(dev, ws_bytes)
+    st = L.aklr_quant_gemm_a8w8_blockscale(
+        p.x.data_ptr(), p.x.stride(0), p.b.data_ptr(), p.b.stride(0) if p.b_layout == _lib.B_ROW_MAJOR else p.k,
+        p.b_scale.data_ptr(), p.b_scale.stride(0), p.bias.data_ptr() if p.bias is not None else None,
+        out.data_ptr(), out.stride(0), p.m, p.n, p.k, p.b_layout, _OUT[p.out_dtype],
+        ws.data_ptr() if ws is not None else None, ws_bytes, _stream(dev),
+    )
+    _lib.check(st, "quant_gemm_a8w8_blockwise_scaled")
+    return out
+
+
+@api("quant_gemm_a8w8_blockwise_scaled@1.0", _run_quant_gemm8)
+def quant_gemm_a8w8_blockwise_scaled(x, b, b_scale, bias=None, out_dtype=None, out=None, *,
+                                     operand_format="none:none"):
+    """``gemm_a8w8_blockwise_scaled(*per_group_quant_fp8(x), b, b_scale, ...)`` in one call, equal bit for
+    bit: bf16 activations x [m, k] are quantized per 1 x 128 group (aklr/ops/quant/reference.py:9-28) and
+    multiplied by the 128 x 128-block-scaled e4m3 weight (aklr/ops/gemm/reference.py:90-105). This is the
+    pair of ops sglang's fp8 block-quant linear calls; for m <= 16 the GEMM's compute waves quantize each K
+    block themselves (one launch, no codes or scales in HBM). b: e4m3fn [n, k] ("none:none") or aiter's 16x16
+    preshuffled layout ("none:preshuffled"); b_scale fp32 [ceil(n/128), k/128]; bias fp32 [n] or None.
+    Calls it does not serve return a ``FallbackReason``."""
+    if not all(isinstance(t, torch.Tensor) for t in (x, b, b_scale)) or (bias is not None and not isinstance(bias, torch.Tensor)):
+        return _OOC
+    b_shuffled = getattr(b, "is_shuffled", False) is True
+    if operand_format == "none:none" and not b_shuffled:
+        variant, b_layout = "row_major", _lib.B_ROW_MAJOR
+    elif operand_format == "none:preshuffled":
+        variant, b_layout = "b_shuffled", _lib.B_PRESHUFFLE_16x16
+    else:
+        return _OOC
+    if x.dtype != torch.bfloat16 or b.dtype != torch.float8_e4m3fn or b_scale.dtype != torch.float32:
+        return _OOC
+    if bias is not None and (bias.dtype != torch.float32 or bias.dim() != 1 or not bias.is_contiguous()):
+        return _OOC
+    dt = _out_dtype(out, out_dtype)
+    if dt is None or x.dim() != 2 or b.dim() != 2 or b_scale.dim() != 2:
+        return _OOC
+    m, k = x.shape
+    n = b.shape[0]
+    if b.shape[1] != k or not (1 <= m <= _MAX_M and 16 <= n <= _MAX_N and n % 16 == 0 and 128 <= k <= _MAX_K
+                               and k % 128 == 0):
+        return _OOC
+    if tuple(b_scale.shape) != (-(-n // 128), k // 128) or not b_scale.is_contiguous():
+        return _OOC
+    if bias is not None and tuple(bias.shape) != (n,):
+        return _OOC
+    if x.stride(1) != 1 or x.stride(0) < k or x.stride(0) % 8 != 0 or not b.is_contiguous():
+        return _OOC
+    if not on_gpu(x, b, b_scale, bias, out):
+        return _OOC
+    if not all(aligned(t) for t in (x, b, b_scale) + ((bias,) if bias is not None else ())):
+        return _OOC
+    if not _out_ok(out, m, n, dt, x.device, (x, b, b_scale, bias)):
+        return _OOC
+    if not workspace.ready(x.device, _lib.lib().aklr_quant_gemm_a8w8_blockscale_workspace_bytes(m, n, k)):
+        return FallbackReason.NOT_WARMED
+    path = "stream_fused" if m <= 16 else ("stream" if m <= 128 else "lds")  # as the library picks
+    return _QuantGemm8Plan(x, b, b_scale, bias, out, dt, m, n, k, b_layout, variant,
+                           f"aklr_quant_gemm_a8w8_blockscale:{path}")
+
+
+# ---------------------------------------------------------------------------------------------
+@dataclass
 class _Gemm4Plan:
     a: torch.Tensor
     b: torch.Tensor

@@ -15,6 +15,9 @@ launch), timed alone with HIP events on its stream over graph replays; peak 8 TB
 roofline.traffic: HBM bytes per launch of that kernel from two rocprofv3 --pmc runs (FETCH_SIZE, then
 WRITE_SIZE) of ``python3 bench.py --probe-traffic``, each scaled by what the counter reads for a plain
 copy of known size in the same run; read from the committed profiles/ summary (null when absent).
+decode_fused_quant: the same step with each pair made one quant_gemm_a8w8_blockwise_scaled call (one
+launch at M <= 16), ms per step and its speedup over the two-op step (an extra: value keeps the
+reference's two-op flow).
 prefill / mxfp4: extra figures (TFLOP/s vs the dense FP8 5.0 PF / MXFP4 10.1 PF peaks): FP8 at
 M in {1024, 4096, 8192}, MXFP4 at M in {1, 32, 512, 4096} (M <= 32 as GB/s vs 8 TB/s).
 quant: the three activation quantizers at H=7168, T in {2048, 16384} (rows a1/a4/a5), next to the
@@ -112,6 +115,24 @@ def build_decode(dev, shuffled=True):
 
     step_bytes = sum(gemm8_bytes(m, n, k) + quant8_bytes(m, k) for (n, k) in shapes for m in ms)
     return step_fn, n_sets, step_bytes, weights, xs
+
+
+def fused_step_fn(weights, xs, shuffled):
+    """The decode step through quant_gemm_a8w8_blockwise_scaled: the same 15 quantize-then-GEMM pairs,
+    one call each (one launch at M <= 16, where the GEMM quantizes its own activations)."""
+    import aklr_amd
+    from aklr_amd import workloads
+
+    fmt = "none:preshuffled" if shuffled else "none:none"
+
+    def step_fn(r):
+        def run():
+            for (n, k) in workloads.DEEPSEEK_NK:
+                b, bs = weights[(n, k)][r % len(weights[(n, k)])]
+                for m in workloads.DECODE_M:
+                    aklr_amd.quant_gemm_a8w8_blockwise_scaled(xs[(m, k)], b, bs, operand_format=fmt)
+        return run
+    return step_fn
 
 
 def time_gemm8(dev, m, n, k, weights, steps, stream, shuffled=True, calls_per_graph=None):
@@ -387,11 +408,17 @@ def main(argv=None):
         return 0
     shuffled = args.layout == "preshuffled"
     print(f"[bench] building decode workload ({args.layout})", file=sys.stderr, flush=True)
-    step_fn, n_sets, step_bytes, weights, _ = build_decode(dev, shuffled)
+    step_fn, n_sets, step_bytes, weights, xs = build_decode(dev, shuffled)
     graphs = [_capture(step_fn(r), stream) for r in range(n_sets)]
     print(f"[bench] {len(graphs)} step graphs captured; timing {args.steps} steps", file=sys.stderr, flush=True)
     ms_per_step = _replay_time_ms(graphs, args.steps, args.warmup, stream)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    del graphs
+    fused_fn = fused_step_fn(weights, xs, shuffled)
+    graphs = [_capture(fused_fn(r), stream) for r in range(n_sets)]
+    ms_fused = _replay_time_ms(graphs, args.steps, args.warmup, stream)
+    print(f"[bench] decode step {ms_per_step:.4f} ms, with the fused quantization {ms_fused:.4f} ms",
+          file=sys.stderr, flush=True)
 
     m_dom, n_dom, k_dom = 16, 7168, 16384
     t_dom = time_gemm8(dev, m_dom, n_dom, k_dom, weights, max(10, args.steps), stream, shuffled)
@@ -406,7 +433,8 @@ def main(argv=None):
     del graphs, weights
     torch.cuda.empty_cache()
 
-    extras = {}
+    extras = {"decode_fused_quant": {"ms_per_step": round(ms_fused, 4),
+                                     "speedup_vs_two_ops": round(ms_per_step / ms_fused, 3)}}
     if not args.no_extras:
         print("[bench] prefill and MXFP4 figures", file=sys.stderr, flush=True)
         extras["prefill_fp8"] = prefill_figures(dev, stream)

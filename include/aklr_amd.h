@@ -112,6 +112,24 @@ int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void* b, int64_t
                               size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * Per-1x128 FP8 quantization of bf16 activations fused into the block-scaled FP8 GEMM:
+ * out = GEMM(per_group_quant_fp8(x), b), equal bit for bit to aklr_per_group_quant_fp8 followed by
+ * aklr_gemm_a8w8_blockscale on its codes and group-major scales (e4m3fn).
+ * Replaces: the pair of calls sglang's fp8 block-quant linear makes on this path,
+ *   per_group_quant_fp8 (aklr/ops/quant/api.py:8-9) then gemm_a8w8_blockwise_scaled
+ *   (aklr/ops/gemm/api.py:32-46), with one launch for m <= 16 (the stream kernel's compute waves
+ *   quantize each K block into LDS); larger m runs the two kernels, the codes and scales in the workspace.
+ * x: bf16 [m, k], row stride ldx elements (multiple of 8). b, b_scale, bias, out as in
+ *   aklr_gemm_a8w8_blockscale. The workspace (aklr_quant_gemm_a8w8_blockscale_workspace_bytes) obeys
+ *   the same rules (16-byte aligned, leading counters zero, left zero).
+ */
+size_t aklr_quant_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k);
+int aklr_quant_gemm_a8w8_blockscale(const void* x, int64_t ldx, const void* b, int64_t ldb, const float* b_scale,
+                                    int64_t ldbs, const float* bias, void* out, int64_t ldo, int64_t m, int64_t n,
+                                    int64_t k, int b_layout, int out_dtype, void* workspace,
+                                    size_t workspace_bytes, hipStream_t stream);
+
+/*
  * MXFP4 GEMM: out = (a * 2^(a_scale-127)) @ (b * 2^(b_scale-127))^T + bias (alpha 1, beta 0).
  * Replaces: gemm_a4w4_mxfp4 kernel ABI `run(a, b, a_scale, b_scale, trans_b, operand_format, alpha,
  *   beta, bias, out_dtype, out)` (call keys per aklr/core/contract/op.py:511-558; no kernel is

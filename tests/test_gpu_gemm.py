@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import aklr_amd
-from aklr_amd import layouts, workloads
+from aklr_amd import layouts, workloads, workspace
 from oracle import gemm as ogemm
 from oracle import quant as oquant
 from tests.helpers import bf16_bits, f32, say, u8
@@ -162,6 +162,47 @@ def test_stream_shapes(m, n, k, bias):
 def test_192_224_column_tiles(m, n, k, bias, fp16):
     _run_and_check(m, n, k, mode="MN", bias=bias, out_dtype=torch.float16 if fp16 else None, seed=61)
     _run_and_check(m, n, k, variant="b_shuffled", bias=False, seed=62)
+
+
+# Fused per-1x128 quantization + GEMM: equal bit for bit to per_group_quant_fp8 then
+# gemm_a8w8_blockwise_scaled, on the fused stream kernel (m <= 16: one row tile, one and two column
+# tiles per wave, K splits, ragged rows and columns, an x row stride past k) and on the two-kernel
+# path beyond (m = 20 .. 300).
+@pytest.mark.parametrize("m,n,k,shuffled,bias,fp16", [
+    (1, 7168, 16384, True, False, False), (16, 7168, 16384, True, False, False), (4, 2112, 7168, True, False, False),
+    (16, 24576, 1536, True, False, False), (13, 4112, 1024, False, True, True), (64, 7168, 2048, True, False, False),
+    (7, 48, 384, False, True, False), (20, 2112, 128, False, False, True), (100, 2112, 7168, True, False, False),
+    (300, 1024, 2048, False, True, False)])
+def test_quant_gemm_fused_matches_two_ops(m, n, k, shuffled, bias, fp16):
+    say(f"quant_gemm_a8w8 m={m} n={n} k={k} shuffled={shuffled} bias={bias} fp16={fp16}")
+    wide = workloads.activations(m, k + 64, seed=71, device=DEV)
+    x = wide[:, 32:32 + k]  # row stride k + 64, 64-byte aligned start
+    b, bs = workloads.blockwise_fp8_weight(n, k, seed=72, device=DEV)
+    bias_t = torch.randn(n, device=DEV, generator=workloads.generator(73, DEV)) if bias else None
+    od = torch.float16 if fp16 else None
+    q, s = aklr_amd.per_group_quant_fp8(x.contiguous())
+    if shuffled:
+        bb = layouts.shuffle_weight(b)
+        ref = aklr_amd.gemm_a8w8_blockwise_scaled(q, bb, s.view(m, k // 128), bs, bias=bias_t, out_dtype=od,
+                                                  operand_format="none:preshuffled") if bias_t is None else None
+        if ref is None:  # the shuffled op variant takes no bias: compare against the row-major op
+            ref = aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s.t().contiguous(), bs, bias=bias_t, out_dtype=od)
+        got = aklr_amd.quant_gemm_a8w8_blockwise_scaled(x, bb, bs, bias=bias_t, out_dtype=od,
+                                                        operand_format="none:preshuffled")
+    else:
+        ref = aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s.t().contiguous(), bs, bias=bias_t, out_dtype=od)
+        got = aklr_amd.quant_gemm_a8w8_blockwise_scaled(x, b, bs, bias=bias_t, out_dtype=od)
+    assert isinstance(got, torch.Tensor) and isinstance(ref, torch.Tensor), (got, ref)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), \
+        f"fused quant+GEMM differs from the two ops: max|diff| {(got.float() - ref.float()).abs().max().item():.3e}"
+    # the shared workspace's split-K counters are zero again (the two-kernel path stages its codes past them)
+    ws = workspace.get(DEV, 1)
+    assert not ws[:65536].any(), "quant_gemm left non-zero split-K counters in the workspace"
+    info = aklr_amd.quant_gemm_a8w8_blockwise_scaled.serving(x, b if not shuffled else bb, bs, bias=bias_t,
+                                                              out_dtype=od,
+                                                              operand_format="none:preshuffled" if shuffled else "none:none")
+    assert info.kernel_ref.endswith(":stream_fused" if m <= 16 else (":stream" if m <= 128 else ":lds"))
 
 
 def test_out_buffer_and_determinism():
