@@ -70,19 +70,26 @@ struct XStage {
   u32x4 v[MT];
 };
 
-template <int MT, int NT, int NW, int D, int NS, int FMT, bool PRE, bool QA = false>
+// KW > 1 splits the workgroup's K range over its waves instead of its columns: the NW compute waves
+// form KW groups of NW / KW, all groups on the same columns, and group kw takes K blocks kb_begin +
+// KW t + kw at step t. A stage then holds KW consecutive K blocks (one per group) and the groups'
+// partial sums meet in LDS at the end, in group order, so a narrow workgroup covers its columns over
+// the whole K range with no split-K partials in memory (the plan then runs one K split).
+template <int MT, int NT, int NW, int D, int NS, int FMT, bool PRE, bool QA = false, int KW = 1>
 __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p) {
-  static_assert(!QA || (MT == 1 && FMT == 0 && NW == 4), "fused quantization: e4m3, one row tile, 4 waves");
-  static_assert(NS >= 2 && D >= 1 && MT >= 1 && MT <= 8 && 128 % (NT * 16) == 0, "stream shape");
-  constexpr int kSRows = (MT * 16 + 63) / 64 * 64;  // a_scale floats per stage: whole 64-lane loads
-  constexpr int kLoadsA = 2 * MT + kSRows / 64;     // loader loads per stage
-  constexpr int kCols = NW * NT * 16;
+  static_assert(!QA || (MT == 1 && FMT == 0 && NW == 4 && KW == 1), "fused quantization: e4m3, one row tile, 4 waves");
+  static_assert(NS >= 2 && D >= 1 && MT >= 1 && MT <= 8 && 128 % (NT * 16) == 0 && NW % KW == 0, "stream shape");
+  constexpr int kSRows = (MT * 16 + 63) / 64 * 64;     // a_scale floats per K block: whole 64-lane loads
+  constexpr int kLoadsA = KW * (2 * MT + kSRows / 64);  // loader loads per stage
+  constexpr int kWC = NW / KW;                          // waves across the columns
+  constexpr int kCols = kWC * NT * 16;
   constexpr int kNBlk = kCols >= 128 ? kCols / 128 : 1;  // 128-column b_scale blocks under the workgroup
   static_assert((NS - 2) * kLoadsA <= 63, "the loader's wait count must fit vmcnt");
-  __shared__ __attribute__((aligned(1024))) uint8_t sA[NS][MT * 2048];
-  __shared__ __attribute__((aligned(16))) float sS[NS][kSRows];
+  __shared__ __attribute__((aligned(1024))) uint8_t sA[NS][KW * MT * 2048];
+  __shared__ __attribute__((aligned(16))) float sS[NS][KW * kSRows];
   __shared__ float sSB[kNBlk][512];
   __shared__ float sQSink[QA ? 64 : 1];  // fused quantization: landing place of the unused scale stores
+  __shared__ f32x4 sRed[KW > 1 ? (NW - kWC) * MT * NT * 64 : 1];  // KW > 1: the groups' partial sums
   __shared__ unsigned arrive_slot;
 
   const int lane = threadIdx.x & 63;
@@ -93,6 +100,8 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   const int KB = p.k >> 7;
   const int kb_begin = split * p.kb_per_split;
   const int kb_end = min(KB, kb_begin + p.kb_per_split);
+  const int steps = (kb_end - kb_begin + KW - 1) / KW;  // K steps (of KW blocks each)
+  const int kw = w / kWC;                               // compute waves: K group
   const int64_t kt32 = p.k >> 5;
 
   f32x4 acc[MT][NT];
@@ -100,7 +109,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int c0w = n0 + w * NT * 16;  // compute wave's first column
+  const int c0w = n0 + (w % kWC) * NT * 16;  // compute wave's first column
   const int col_w = c0w + 4 * g;     // + nt * 16: the lane's first output column
   // split-K partials: one plane per split of gridDim.x * NW * MT * NT 1 KiB tiles (fp32 elements)
   const int64_t stream_plane = (int64_t)gridDim.x * NW * MT * NT * 256;
@@ -134,25 +143,30 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
       s_off[i] = row < p.m ? (uint32_t)((int64_t)row * p.sa_sm * 4) : kOobOffset;
     }
     const uint32_t lds_a0 = lds_addr(&sA[0][0]), lds_s0 = lds_addr(&sS[0][0]);
-    auto issue = [&](int kb, int st) {
-      const bool on = kb < kb_end;
-      const uint32_t ak = (uint32_t)kb * 128u, sk = (uint32_t)kb * (uint32_t)(p.sa_sk * 4);
+    auto issue = [&](int t, int st) {  // step t: blocks kb_begin + KW t + j, j < KW
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int j = 0; j < KW; ++j) {
+        const int kb = kb_begin + KW * t + j;
+        const bool on = kb < kb_end;
+        const uint32_t ak = (uint32_t)kb * 128u, sk = (uint32_t)kb * (uint32_t)(p.sa_sk * 4);
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-          lds_dma16(ars, lds_a0 + st * (MT * 2048) + mt * 2048 + h * 1024,
-                    on && a_off[mt] != kOobOffset ? a_off[mt] + ak + 64 * h : kOobOffset);
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int i = 0; i < kSRows / 64; ++i)
-        lds_dma4(sars, lds_s0 + st * (kSRows * 4) + i * 256, on && s_off[i] != kOobOffset ? s_off[i] + sk : kOobOffset);
+          for (int h = 0; h < 2; ++h)
+            lds_dma16(ars, lds_a0 + st * (KW * MT * 2048) + (j * MT + mt) * 2048 + h * 1024,
+                      on && a_off[mt] != kOobOffset ? a_off[mt] + ak + 64 * h : kOobOffset);
+#pragma unroll
+        for (int i = 0; i < kSRows / 64; ++i)
+          lds_dma4(sars, lds_s0 + (st * KW + j) * (kSRows * 4) + i * 256,
+                   on && s_off[i] != kOobOffset ? s_off[i] + sk : kOobOffset);
+      }
     };
     // Stage kb lives in slot (kb - kb_begin) % NS, and all NS slots start filled. A first barrier
     // publishes stage kb_begin; then barrier kb publishes stage kb + 1 (the loader's own loads of it
     // have landed, NS - 2 younger stages stay in flight), and by then every compute wave has read
     // stage kb -- fragments are read one K block ahead -- so its slot takes stage kb + NS. Issues past
     // the K range load zeros, which keeps the count exact.
-    issue(kb_begin, 0);
+    issue(0, 0);
     // b_scale of the workgroup's column blocks over its K range (kb_per_split <= 512), staged once,
     // behind the first A stage; the first stage barrier publishes it with stage 0.
     {
@@ -165,13 +179,13 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage 0 and b_scale have landed
 #pragma unroll
-    for (int s = 1; s < NS; ++s) issue(kb_begin + s, s);  // only stage loads from here: the counts are exact
+    for (int s = 1; s < NS; ++s) issue(s, s);  // only stage loads from here: the counts are exact
     stage_barrier();
     int st_fill = 0;
-    for (int kb = kb_begin; kb < kb_end; ++kb) {
+    for (int t = 0; t < steps; ++t) {
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * kLoadsA) : "memory");
       stage_barrier();
-      issue(kb + NS, st_fill);
+      issue(t + NS, st_fill);
       st_fill = st_fill + 1 == NS ? 0 : st_fill + 1;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -188,8 +202,11 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     }
     const uint32_t b_lane = PRE ? (uint32_t)((g >> 1) * 512 + (g & 1) * 256 + li * 16)
                                 : (uint32_t)(li * p.ldb + g * 16);
+    // Step counter kb runs kb_begin, kb_begin + 1, ...; this wave's K block at step kb is kbw(kb).
+    auto kbw = [&](int kb) { return KW == 1 ? kb : kb_begin + KW * (kb - kb_begin) + kw; };
     auto load = [&](int kb, StreamFrag<NT>& f) {
-      const uint32_t boff = kb < kb_end ? (uint32_t)(PRE ? kb * 2048 : kb * 128) : kOobOffset;
+      const int kb_w = kbw(kb);
+      const uint32_t boff = kb_w < kb_end ? (uint32_t)(PRE ? kb_w * 2048 : kb_w * 128) : kOobOffset;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
         f.b[nt] = cat(buf_ld16<kNt>(brs[nt], b_lane + boff), buf_ld16<kNt>(brs[nt], b_lane + boff + (PRE ? 1024 : 64)));
@@ -252,12 +269,25 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
       // step into blocks and let the compiler sink the step's MFMAs past the following barriers
       *(qp == 0 ? &sS[slot][qrow] : &sQSink[lane]) = sc;
     };
+    // D-deep ring: block kb_begin + i lives in slot i % D. Its first D blocks go out at once, before
+    // the first stage barrier, so the weight stream starts with the kernel rather than one round trip
+    // (the loader's first stage) later. The x ring's loads go out just ahead of the weight loads of the
+    // same slot, in the order the steps issue them, so that the loop head sees one order of outstanding
+    // loads and waits for no more than the slot it consumes.
+    StreamFrag<NT> f[D];
     XStage<MT> xr[QA ? D : 1];
+    XStage<MT> pro[QA ? NS : 1];
     if constexpr (QA) {
-      // every slot starts filled: stages kb_begin .. kb_begin + NS - 1, loaded together
-      XStage<MT> pro[NS];
+      // every slot starts filled: stages kb_begin .. kb_begin + NS - 1, loaded first
 #pragma unroll
       for (int s0 = 0; s0 < NS; ++s0) xload(kb_begin + s0, pro[s0]);
+    }
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      if constexpr (QA) xload(kb_begin + NS + j, xr[j]);
+      load(kb_begin + j, f[j]);
+    }
+    if constexpr (QA) {
 #pragma unroll
       for (int s0 = 0; s0 < NS; ++s0) qwrite(pro[s0], s0);
     }
@@ -270,9 +300,9 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     i32x8 af[MT];
     float s[MT];
     auto read_frags = [&](int mt, int slot) {
-      af[mt] = cat(*reinterpret_cast<const u32x4*>(&sA[slot][mt * 2048 + lane * 16]),
-                   *reinterpret_cast<const u32x4*>(&sA[slot][mt * 2048 + 1024 + lane * 16]));
-      s[mt] = sS[slot][mt * 16 + li];
+      af[mt] = cat(*reinterpret_cast<const u32x4*>(&sA[slot][(kw * MT + mt) * 2048 + lane * 16]),
+                   *reinterpret_cast<const u32x4*>(&sA[slot][(kw * MT + mt) * 2048 + 1024 + lane * 16]));
+      s[mt] = sS[slot][kw * kSRows + mt * 16 + li];
     };
     stage_barrier();  // publishes stage kb_begin
 #pragma unroll
@@ -290,7 +320,8 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
         __builtin_amdgcn_sched_barrier(0);
       }
       st = st + 1 == NS ? 0 : st + 1;
-      const float sb = sbw[kb - kb_begin];
+      // a group's blocks past the K range hold zeros; their b_scale slot was never staged
+      const float sb = KW == 1 ? sbw[kb - kb_begin] : (kbw(kb) < kb_end ? sbw[kbw(kb) - kb_begin] : 0.0f);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const float sc = s[mt] * sb;
@@ -315,19 +346,10 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
       __builtin_amdgcn_sched_barrier(0);  // refill this slot before consuming the next
     };
 
-    // D-deep ring: block kb_begin + i lives in slot i % D. Whole groups of D blocks run in a loop with
-    // no exit inside (its head then has one ring state, and the compiler waits for exactly the slot
-    // it consumes); the remaining < D blocks follow, one guarded step each.
-    // The x ring's loads go out just ahead of the weight loads of the same slot, in the order the steps
-    // issue them, so that the loop head sees one order of outstanding loads and waits for no more
-    // than the slot it consumes.
-    StreamFrag<NT> f[D];
-#pragma unroll
-    for (int j = 0; j < D; ++j) {
-      if constexpr (QA) xload(kb_begin + NS + j, xr[j]);
-      load(kb_begin + j, f[j]);
-    }
-    const int len = kb_end - kb_begin, full = len / D * D;
+    // Whole groups of D blocks run in a loop with no exit inside (its head then has one ring state, and
+    // the compiler waits for exactly the slot it consumes); the remaining < D blocks follow, one guarded
+    // step each.
+    const int len = steps, full = len / D * D;
     for (int kb0 = kb_begin; kb0 < kb_begin + full; kb0 += D) {
 #pragma unroll
       for (int j = 0; j < D; ++j) step(kb0 + j, f[j], xr[QA ? j : 0]);
@@ -345,6 +367,24 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) store_partial4(prs, part_base + (mt * NT + nt) * 256, acc[mt][nt]);
     }
+  }
+
+  if constexpr (KW > 1) {
+    // The K groups' sums meet in LDS and group 0 adds them in group order (the plan runs one K split).
+    if (w < NW && kw > 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) sRed[(((w - kWC) * MT + mt) * NT + nt) * 64 + lane] = acc[mt][nt];
+    }
+    __syncthreads();
+    if (w == NW || kw > 0) return;
+#pragma unroll
+    for (int j = 1; j < KW; ++j)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] += sRed[((((j - 1) * kWC + w) * MT + mt) * NT + nt) * 64 + lane];
   }
 
   if (p.splits > 1) {
@@ -731,6 +771,7 @@ enum class Kernel8 { kStream, kLds };
 struct Plan8 {
   Kernel8 kind;
   int mt, nt, nw;    // stream: 16-row and 16-column tiles per wave, compute waves per workgroup
+  int kw;            // stream: K groups among the compute waves (1: the waves split the columns)
   int tm, tn;        // lds: workgroup tile
   int grid_x;        // stream: column groups; lds: output tiles
   int splits, kb_per_split;
@@ -749,6 +790,7 @@ static Plan8 plan8_lds(int64_t m, int64_t n, int64_t k, int tm, int tn, int64_t 
   Plan8 p;
   p.kind = Kernel8::kLds;
   p.mt = p.nt = p.nw = 0;
+  p.kw = 1;
   p.tm = tm;
   p.tn = tn;
   const int64_t KB = k / 128;
@@ -818,12 +860,31 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k) {
   p.mt = m <= 16 ? 1 : (m <= 32 ? 2 : (m <= 64 ? 4 : 8));
   p.nt = n >= 4096 && (m > 16 || (n + 63) / 64 > 256) ? 2 : 1;
   p.nw = 4;
+  p.kw = 1;
   const int64_t groups = (n + 64 * p.nt - 1) / (64 * p.nt);
   p.grid_x = (int)groups;
   int64_t s = 256 / groups;
   if (s > 4) s = 4;
   if (s > KB / 4) s = KB / 4;
   finish_splits(p, KB, s);
+  // Where that plan splits K over workgroups and K is short, the waves split K instead: 2 or 4 K
+  // groups of one 16-column tile each, the smaller count that still makes >= 200 workgroups, one K
+  // split, no partials in memory. Measured at m = 1, 16 and 32 (16-row tiles: 1, 1, 2): N x K =
+  // 4096 x 8192 10.9 -> 9.1 us (m = 1), 4096 x 4096 7.4 -> 6.3, 7168 x 2048 6.9 -> 5.6, 8192 x 1024
+  // 5.6 -> 4.4 (m = 32: 7.4 -> 5.4). Longer K (7168 x 16384: 128 K blocks) amortizes the split-K
+  // epilogue and keeps the split plan; at 2 row tiles the wave split loses beyond 32 K blocks.
+  if (p.mt <= 2 && p.splits > 1 && KB <= (p.mt == 1 ? 64 : 32)) {
+    for (int kw = 2; kw <= 4; kw *= 2) {
+      const int64_t wgs = (n + 64 / kw - 1) / (64 / kw);
+      if (wgs >= 200) {
+        p.kw = kw;
+        p.nt = 1;
+        p.grid_x = (int)wgs;
+        finish_splits(p, KB, 1);
+        break;
+      }
+    }
+  }
   return p;
 }
 
@@ -841,16 +902,19 @@ static size_t workspace8(const Plan8& p) {
 }
 
 // Stream kernel: 4 compute waves and 4 A stages; ring depth 4 at 1-2 row tiles, else 2 (measured).
-template <int MT, int NT, int FMT, bool PRE, bool QA = false>
+template <int MT, int NT, int FMT, bool PRE, bool QA = false, int KW = 1>
 static void launch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   constexpr int D = MT <= 2 ? 4 : 2;
-  hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, 4, D, 4, FMT, PRE, QA>),
+  hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, 4, D, 4, FMT, PRE, QA, KW>),
                      dim3((unsigned)d.grid_x, (unsigned)d.splits), dim3(5 * 64), 0, s, a);
 }
 
 template <int FMT, bool PRE>
 static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
-  if (d.mt == 1) d.nt == 2 ? launch_stream<1, 2, FMT, PRE>(a, d, s) : launch_stream<1, 1, FMT, PRE>(a, d, s);
+  if (d.kw > 1) {  // one column tile per wave, 1 or 2 row tiles
+    if (d.mt == 1) d.kw == 2 ? launch_stream<1, 1, FMT, PRE, false, 2>(a, d, s) : launch_stream<1, 1, FMT, PRE, false, 4>(a, d, s);
+    else d.kw == 2 ? launch_stream<2, 1, FMT, PRE, false, 2>(a, d, s) : launch_stream<2, 1, FMT, PRE, false, 4>(a, d, s);
+  } else if (d.mt == 1) d.nt == 2 ? launch_stream<1, 2, FMT, PRE>(a, d, s) : launch_stream<1, 1, FMT, PRE>(a, d, s);
   else if (d.mt == 2) d.nt == 2 ? launch_stream<2, 2, FMT, PRE>(a, d, s) : launch_stream<2, 1, FMT, PRE>(a, d, s);
   else if (d.mt == 4) d.nt == 2 ? launch_stream<4, 2, FMT, PRE>(a, d, s) : launch_stream<4, 1, FMT, PRE>(a, d, s);
   else d.nt == 2 ? launch_stream<8, 2, FMT, PRE>(a, d, s) : launch_stream<8, 1, FMT, PRE>(a, d, s);
@@ -860,7 +924,7 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
 // the workspace and runs the GEMM. Measured on the DeepSeek-V3 shapes: one row tile saves 1-1.5 us a
 // call over the two launches; at 2 row tiles (8 values a lane) the two are even, at 4 (32 values a
 // lane) the quantization outgrows the wait for the weights and the fused call is 15-25% slower.
-static bool fused_quant_ok(const Plan8& p) { return p.kind == Kernel8::kStream && p.mt == 1; }
+static bool fused_quant_ok(const Plan8& p) { return p.kind == Kernel8::kStream && p.mt == 1 && p.kw == 1; }
 
 template <bool PRE>
 static void dispatch_stream_qa(const Gemm8Args& a, const Plan8& d, hipStream_t s) {

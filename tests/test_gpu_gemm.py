@@ -106,6 +106,29 @@ def test_decode_b_shuffled(m, nk):
     _run_and_check(m, n, k, variant="b_shuffled", rows=128, cols=1024, seed=m + 100)
 
 
+# Stream plans whose waves split K (2 or 4 K groups of one column tile, one K split): K ranges that are
+# whole multiples of the group count and ones that leave a group's last block past the range (k = 1152:
+# 9 blocks over 2 groups; k = 1408: 11 over 4), 1 and 2 row tiles, ragged n, both weight layouts,
+# bias and fp16 output. The plan for each is in the comment.
+@pytest.mark.parametrize("m,n,k,variant,bias,fp16", [
+    (1, 4096, 8192, "b_shuffled", False, False),    # 4 groups, 64 blocks
+    (16, 4096, 4096, "row_major", True, False),     # 4 groups
+    (5, 7168, 2048, "b_shuffled", False, True),     # 2 groups
+    (32, 8192, 1024, "row_major", False, False),    # 2 groups, 2 row tiles
+    (20, 4096, 2048, "b_shuffled", False, False),   # 4 groups, 2 row tiles
+    (3, 8192, 1152, "row_major", False, False),     # 2 groups, 9 blocks
+    (16, 4096, 1408, "b_shuffled", False, False),   # 4 groups, 11 blocks
+    (9, 4112, 4096, "row_major", True, True),       # 4 groups, 257 workgroups, ragged last tile
+])
+def test_wave_split_k_plans(m, n, k, variant, bias, fp16):
+    out = _run_and_check(m, n, k, variant=variant, bias=bias, out_dtype=torch.float16 if fp16 else None,
+                         seed=m + 300, rows=64, cols=min(n, 2048))
+    if m == 1:  # the groups' sums meet in a fixed order: bitwise reproducible
+        again = _run_and_check(m, n, k, variant=variant, seed=m + 300, rows=8, cols=64)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+
+
 @pytest.mark.parametrize("nk", workloads.DEEPSEEK_NK)
 @pytest.mark.parametrize("m", workloads.PREFILL_M)
 def test_prefill_row_major(m, nk):
