@@ -59,12 +59,14 @@ struct StreamFrag {
   i32x8 b[NT];
 };
 
-// Fused activation quantization (QA, MT <= 4): p.a is then bf16 x [m, lda elements], and the compute
-// waves quantize each K block of it per 1 x 128 group with the arithmetic of quant_fp8_1x128_kernel
-// (amax floored at 1e-10, s = amax * fl(1/448), codes e4m3(clamp(x * (1/s)))), writing the codes in
-// fragment order and s into the stage: the LDS stage holds exactly the bytes the loader would have
-// moved from per_group_quant_fp8's output. Compute wave w quantizes rows [4 MT w, 4 MT (w + 1)) of
-// the MT * 16: 16 / MT lanes per row, 8 MT values (MT 16-byte loads) per lane.
+// Fused activation quantization (QA, one row tile): p.a is then bf16 x [m, lda elements], and the
+// compute waves quantize each K block of it per 1 x 128 group with the arithmetic of
+// quant_fp8_1x128_kernel (amax floored at 1e-10, s = amax * fl(1/448), codes e4m3(clamp(x * (1/s)))),
+// writing the codes in fragment order and s into the stage: the LDS stage holds exactly the bytes the
+// loader would have moved from per_group_quant_fp8's output. Compute wave w quantizes rows
+// [4w, 4w + 4) of the 16: 16 lanes per row, 8 values (one 16-byte load) per lane. (The index
+// arithmetic is written for MT row tiles, 16 / MT lanes per row; only MT = 1 is instantiated, being
+// the only row count at which the fused kernel beats the two launches.)
 template <int MT>
 struct XStage {
   u32x4 v[MT];
