@@ -1,6 +1,6 @@
 // Dynamic activation quantizers for gfx950: per-1x128 FP8 (fp32 scales, group-major), per-1x32
 // MXFP8 (e8m0 scales) and per-1x32 MXFP4 (e2m1 codes, e8m0 scales, row-major or aiter-shuffled).
-// All three are HBM-bound: one coalesced pass over x, amax reduced with lane shuffles inside the
+// All three are HBM-bound: one coalesced pass over x, amax reduced with DPP lane moves inside the
 // lanes that share a group, codes and scales written once.
 #include "common.h"
 
@@ -51,9 +51,10 @@ __global__ __launch_bounds__(256) void quant_fp8_1x128_kernel(const uint16_t* __
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(f[i]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
-  amax = fmaxf(amax, __shfl_xor(amax, 2));
-  amax = fmaxf(amax, __shfl_xor(amax, 4));
+  // the 8 lanes of a row are one half DPP row: quad swaps, then the half-row mirror (no LDS permutes)
+  amax = fmaxf(amax, dpp_f32<0xB1>(amax));   // quad_perm [1,0,3,2]
+  amax = fmaxf(amax, dpp_f32<0x4E>(amax));   // quad_perm [2,3,0,1]
+  amax = fmaxf(amax, dpp_f32<0x141>(amax));  // row_half_mirror
   amax = fmaxf(amax, kAmaxFloor);
   const float s = amax * kInv448;   // rounds once to fp32
   const float inv = 1.0f / s;       // IEEE division: correctly rounded (no fast-math in this build)
@@ -96,8 +97,8 @@ __device__ __forceinline__ Group32 unpack_group32(const u32x4& v) {
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(g.f[i]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
-  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  amax = fmaxf(amax, dpp_f32<0xB1>(amax));  // the group's 4 lanes are one quad: quad_perm [1,0,3,2]
+  amax = fmaxf(amax, dpp_f32<0x4E>(amax));  // quad_perm [2,3,0,1]
   g.amax = amax;
   return g;
 }
