@@ -861,6 +861,11 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k) {
   const int64_t KB = k / 128;
   p.mt = m <= 16 ? 1 : (m <= 32 ? 2 : (m <= 64 ? 4 : 8));
   p.nt = n >= 4096 && (m > 16 || (n + 63) / 64 > 256) ? 2 : 1;
+  // At 4 and 8 row tiles and K <= 64 blocks, one column tile per wave while that leaves <= 256 column
+  // groups: twice the workgroups or half the K splits (measured, us, two tiles -> one: 7168 x 2048
+  // 11.5 -> 9.4 at m = 64 and 15.7 -> 13.4 at m = 128; 4096 x 8192 16.6 -> 14.2 and 22.0 -> 19.0). Longer
+  // K keeps two (7168 x 16384 at m = 128: 38 vs 47 us, the narrower groups re-reading A from L2).
+  if (p.mt >= 4 && KB <= 64 && (n + 63) / 64 <= 256) p.nt = 1;
   p.nw = 4;
   p.kw = 1;
   const int64_t groups = (n + 64 * p.nt - 1) / (64 * p.nt);

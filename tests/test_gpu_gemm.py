@@ -129,6 +129,19 @@ def test_wave_split_k_plans(m, n, k, variant, bias, fp16):
         assert torch.equal(out.view(torch.int16), again.view(torch.int16))
 
 
+# Stream plans at 4 and 8 row tiles with one column tile per wave (K <= 64 blocks, <= 256 column groups):
+# both layouts, bias, fp16 output, a ragged last column group and ragged rows.
+@pytest.mark.parametrize("m,n,k,variant,bias,fp16", [
+    (64, 7168, 2048, "b_shuffled", False, False),
+    (128, 4096, 8192, "row_major", True, False),
+    (100, 4112, 4096, "b_shuffled", False, False),
+    (50, 8192, 1024, "row_major", False, True),
+])
+def test_stream_one_column_tile_plans(m, n, k, variant, bias, fp16):
+    _run_and_check(m, n, k, variant=variant, bias=bias, out_dtype=torch.float16 if fp16 else None, seed=m + 500,
+                   rows=64, cols=min(n, 2048))
+
+
 @pytest.mark.parametrize("nk", workloads.DEEPSEEK_NK)
 @pytest.mark.parametrize("m", workloads.PREFILL_M)
 def test_prefill_row_major(m, nk):
