@@ -1055,6 +1055,11 @@ extern "C" size_t aklr_quant_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int
   return quant_gemm_workspace(plan8(m, n, k), m, k);
 }
 
+extern "C" int aklr_quant_gemm_a8w8_blockscale_fused(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k < 128) return 0;
+  return fused_quant_ok(plan8(m, n, k)) ? 1 : 0;
+}
+
 extern "C" int aklr_quant_gemm_a8w8_blockscale(const void* x, int64_t ldx, const void* b, int64_t ldb,
                                                const float* b_scale, int64_t ldbs, const float* bias, void* out,
                                                int64_t ldo, int64_t m, int64_t n, int64_t k, int b_layout,

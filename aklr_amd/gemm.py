@@ -268,7 +268,8 @@ def quant_gemm_a8w8_blockwise_scaled(x, b, b_scale, bias=None, out_dtype=None, o
         return _OOC
     if not workspace.ready(x.device, _lib.lib().aklr_quant_gemm_a8w8_blockscale_workspace_bytes(m, n, k)):
         return FallbackReason.NOT_WARMED
-    path = "stream_fused" if m <= 16 else ("stream" if m <= 128 else "lds")  # as the library picks
+    fused = _lib.lib().aklr_quant_gemm_a8w8_blockscale_fused(m, n, k) == 1  # as the library picks
+    path = "stream_fused" if fused else ("stream" if m <= 128 else "lds")
     return _QuantGemm8Plan(x, b, b_scale, bias, out, dt, m, n, k, b_layout, variant,
                            f"aklr_quant_gemm_a8w8_blockscale:{path}")
 

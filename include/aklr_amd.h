@@ -124,6 +124,9 @@ int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void* b, int64_t
  *   the same rules (16-byte aligned, leading counters zero, left zero).
  */
 size_t aklr_quant_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k);
+/* 1 when aklr_quant_gemm_a8w8_blockscale runs (m, n, k) as one launch, 0 when as the two kernels
+ * (a query for callers that report which kernel serves a call; no counterpart in the reference). */
+int aklr_quant_gemm_a8w8_blockscale_fused(int64_t m, int64_t n, int64_t k);
 int aklr_quant_gemm_a8w8_blockscale(const void* x, int64_t ldx, const void* b, int64_t ldb, const float* b_scale,
                                     int64_t ldbs, const float* bias, void* out, int64_t ldo, int64_t m, int64_t n,
                                     int64_t k, int b_layout, int out_dtype, void* workspace,

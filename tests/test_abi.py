@@ -78,3 +78,17 @@ def test_workspace_sizes_are_host_computable(native_lib):
         # workgroups at most 256 x 256
         assert ws % 1024 == 0 and ws <= 65536 + 8 * up(m, 256) * up(n, 256) * 4
     assert L.aklr_gemm_a4w4_mxfp4_workspace_bytes(1, 10240, 8192) % 4 == 0
+
+
+def test_quant_gemm_path_and_workspace_are_host_computable(native_lib):
+    L = native_lib
+    fused = L.aklr_quant_gemm_a8w8_blockscale_fused
+    # one launch at one row tile on the decode shapes; two kernels past 16 rows, on a wave-split-K plan
+    # (4096 x 8192) and for empty sizes
+    assert fused(16, 7168, 16384) == 1 and fused(1, 2112, 7168) == 1 and fused(4, 24576, 1536) == 1
+    assert fused(17, 7168, 16384) == 0 and fused(300, 1024, 2048) == 0
+    assert fused(1, 4096, 8192) == 0
+    assert fused(0, 7168, 16384) == 0 and fused(1, 7168, 64) == 0
+    # the two-kernel path stages the codes and scales past the 64 KiB counter region
+    m, n, k = 20, 2112, 128
+    assert L.aklr_quant_gemm_a8w8_blockscale_workspace_bytes(m, n, k) >= 65536 + m * k + (k // 128) * m * 4
