@@ -73,10 +73,11 @@ struct XStage {
 };
 
 // KW > 1 splits the workgroup's K range over its waves instead of its columns: the NW compute waves
-// form KW groups of NW / KW, all groups on the same columns, and group kw takes K blocks kb_begin +
-// KW t + kw at step t. A stage then holds KW consecutive K blocks (one per group) and the groups'
-// partial sums meet in LDS at the end, in group order, so a narrow workgroup covers its columns over
-// the whole K range with no split-K partials in memory (the plan then runs one K split).
+// form KW groups of NW / KW, all groups on the same columns, and group kw takes the contiguous K blocks
+// [kb_begin + kw * steps, + steps) (steps = the range over KW, rounded up), one per step. A stage then
+// holds one K block per group and the groups' partial sums meet in LDS at the end, in group order, so
+// a narrow workgroup covers its columns over the whole K range with no split-K partials in memory (the
+// plan then runs one K split).
 template <int MT, int NT, int NW, int D, int NS, int FMT, bool PRE, bool QA = false, int KW = 1>
 __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p) {
   static_assert(!QA || (MT == 1 && FMT == 0 && NW == 4 && KW == 1), "fused quantization: e4m3, one row tile, 4 waves");
@@ -145,11 +146,11 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
       s_off[i] = row < p.m ? (uint32_t)((int64_t)row * p.sa_sm * 4) : kOobOffset;
     }
     const uint32_t lds_a0 = lds_addr(&sA[0][0]), lds_s0 = lds_addr(&sS[0][0]);
-    auto issue = [&](int t, int st) {  // step t: blocks kb_begin + KW t + j, j < KW
+    auto issue = [&](int t, int st) {  // step t: group j's block t, j < KW
 #pragma unroll
       for (int j = 0; j < KW; ++j) {
-        const int kb = kb_begin + KW * t + j;
-        const bool on = kb < kb_end;
+        const int kb = kb_begin + j * steps + t;  // group j's blocks are [kb_begin + j steps, + steps)
+        const bool on = t < steps && kb < kb_end;
         const uint32_t ak = (uint32_t)kb * 128u, sk = (uint32_t)kb * (uint32_t)(p.sa_sk * 4);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
@@ -205,10 +206,11 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     const uint32_t b_lane = PRE ? (uint32_t)((g >> 1) * 512 + (g & 1) * 256 + li * 16)
                                 : (uint32_t)(li * p.ldb + g * 16);
     // Step counter kb runs kb_begin, kb_begin + 1, ...; this wave's K block at step kb is kbw(kb).
-    auto kbw = [&](int kb) { return KW == 1 ? kb : kb_begin + KW * (kb - kb_begin) + kw; };
+    auto kbw = [&](int kb) { return KW == 1 ? kb : kb_begin + kw * steps + (kb - kb_begin); };
     auto load = [&](int kb, StreamFrag<NT>& f) {
       const int kb_w = kbw(kb);
-      const uint32_t boff = kb_w < kb_end ? (uint32_t)(PRE ? kb_w * 2048 : kb_w * 128) : kOobOffset;
+      const bool on = kb_w < kb_end && (KW == 1 || kb - kb_begin < steps);
+      const uint32_t boff = on ? (uint32_t)(PRE ? kb_w * 2048 : kb_w * 128) : kOobOffset;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
         f.b[nt] = cat(buf_ld16<kNt>(brs[nt], b_lane + boff), buf_ld16<kNt>(brs[nt], b_lane + boff + (PRE ? 1024 : 64)));
