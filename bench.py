@@ -20,10 +20,12 @@ launch at M <= 16), ms per step and its speedup over the two-op step (an extra: 
 reference's two-op flow).
 reference_recorded_fp8: the FP8 GEMM on the 17 shapes whose times the reference records in its kernel
 schema files (its CI: graph replay after a 1 GiB cache flush, median), next to those times. Here each call
-runs on cold operands too (rotating > 512 MB of copies), and the figure is the median of 7 replays. Below ~10 us the reference's figure includes its
+runs on cold operands too (rotating > 512 MB of copies), and the figure is the median of 7 replays after
+>= 50 ms of warm-up replays. Below ~10 us the reference's figure includes its
 timer's ~4.2 us floor, so only the larger shapes compare kernels.
 prefill / mxfp4: extra figures (TFLOP/s vs the dense FP8 5.0 PF / MXFP4 10.1 PF peaks): FP8 at
-M in {1024, 4096, 8192}, MXFP4 at M in {1, 32, 512, 4096} (M <= 32 as GB/s vs 8 TB/s).
+M in {1024, 4096, 8192} (median of 10 launches after >= 50 ms of warm-up launches), MXFP4 at M in
+{1, 32, 512, 4096} (M <= 32 as GB/s vs 8 TB/s).
 quant: the three activation quantizers at H=7168, T in {2048, 16384} (rows a1/a4/a5), next to the
 reference's recorded times where it has them.
 moe: the grouped DeepSeek-V3 FP8 MoE experts (256 routed + 1 shared, top-8,
@@ -78,10 +80,17 @@ def _replay_time_ms(graphs, steps, warmup, stream):
     return start.elapsed_time(end) / steps
 
 
-def _replay_median_ms(graph, reps, warmup, stream):
-    """Median over ``reps`` single replays of ``graph``, each timed with HIP events on ``stream``."""
-    for _ in range(warmup):
+def _replay_median_ms(graph, reps, warmup, stream, warm_ms=50.0):
+    """Median over ``reps`` single replays of ``graph``, each timed with HIP events on ``stream``, after
+    ``warmup`` replays and at least ``warm_ms`` of them (the clocks settle under sustained load: the first
+    milliseconds of a compute-bound shape run up to 15% slower)."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or (time.perf_counter() - t0) * 1e3 < warm_ms:
         graph.replay()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     times = []
     for _ in range(reps):
@@ -193,7 +202,7 @@ def prefill_figures(dev, stream, steps=10):
         bsh = layouts.shuffle_weight(b)
         g = _capture(lambda: aklr_amd.gemm_a8w8_blockwise_scaled(q, bsh, s.view(m, k // 128), bs,
                                                                  operand_format="none:preshuffled"), stream)
-        t = _replay_time_ms([g], steps, 2, stream)
+        t = _replay_median_ms(g, steps, 2, stream)
         tf = 2.0 * m * n * k / (t * 1e-3) / 1e12
         out.append({"m": m, "n": n, "k": k, "us": round(t * 1e3, 2), "tflops": round(tf, 1),
                     "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)})
