@@ -477,8 +477,8 @@ def cpu_baseline():
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layout", choices=("preshuffled", "row_major"), default="preshuffled")
     ap.add_argument("--no-extras", action="store_true", help="skip the prefill/MXFP4 figures")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
