@@ -170,6 +170,13 @@ def test_e5m2(m):
     _run_and_check(m, 1024, 2048, dtype=torch.float8_e5m2, seed=31)
 
 
+# e5m2 on the wave-split-K plan (m = 16, 4096 x 4096: 4 K groups) and on one column tile per wave at 4 row
+# tiles (m = 64, 7168 x 2048)
+@pytest.mark.parametrize("m,n,k", [(16, 4096, 4096), (64, 7168, 2048)])
+def test_e5m2_stream_plans(m, n, k):
+    _run_and_check(m, n, k, dtype=torch.float8_e5m2, seed=33, rows=64, cols=1024)
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 16, 128), (129, 48, 128), (17, 2112, 256), (130, 144, 384),
                                    (1, 16, 65536), (16, 256, 16384), (33, 64, 8192),
                                    (513, 2112, 256), (600, 144, 384), (1000, 48, 1024)])
