@@ -253,6 +253,34 @@ def test_quant_gemm_fused_matches_two_ops(m, n, k, shuffled, bias, fp16):
     assert info.kernel_ref.endswith(":stream_fused" if fused else (":stream" if m <= 128 else ":lds"))
 
 
+def test_quant_gemm_into_strided_out():
+    # out= through the op (contiguous, as its contract takes it), then a column slice of a wider buffer
+    # through the C ABI's row stride: the fused path (m = 4) and the two-kernel path (m = 40); the columns
+    # around the slice stay untouched
+    L = aklr_amd._lib.lib()
+    for m in (4, 40):
+        n, k = 2112, 7168
+        x = workloads.activations(m, k, seed=81, device=DEV)
+        b, bs = workloads.blockwise_fp8_weight(n, k, seed=82, device=DEV)
+        bb = layouts.shuffle_weight(b)
+        q, s = aklr_amd.per_group_quant_fp8(x)
+        ref = aklr_amd.gemm_a8w8_blockwise_scaled(q, bb, s.view(m, k // 128), bs, operand_format="none:preshuffled")
+        out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+        got = aklr_amd.quant_gemm_a8w8_blockwise_scaled(x, bb, bs, out=out, operand_format="none:preshuffled")
+        assert got is out
+        wide = torch.full((m, n + 64), float("nan"), dtype=torch.bfloat16, device=DEV)
+        ws_bytes = L.aklr_quant_gemm_a8w8_blockscale_workspace_bytes(m, n, k)
+        ws = torch.zeros(max(ws_bytes, 16), dtype=torch.uint8, device=DEV)
+        st = L.aklr_quant_gemm_a8w8_blockscale(x.data_ptr(), k, bb.data_ptr(), k, bs.data_ptr(), bs.stride(0), None,
+                                               wide[:, 32:].data_ptr(), n + 64, m, n, k, aklr_amd._lib.B_PRESHUFFLE_16x16,
+                                               0, ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
+        assert st == 0
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+        assert torch.equal(wide[:, 32:32 + n].view(torch.int16), ref.view(torch.int16))
+        assert torch.isnan(wide[:, :32].float()).all() and torch.isnan(wide[:, 32 + n:].float()).all()
+
+
 def test_out_buffer_and_determinism():
     m, n, k = 64, 7168, 16384
     q, s, b, bs = _fp8_inputs(m, n, k, seed=5)
