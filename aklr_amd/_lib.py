@@ -62,6 +62,7 @@ SIGNATURES: dict[str, tuple] = {
 # enums of include/aklr_amd.h
 AKLR_OK = 0
 AKLR_ERR_INVALID_ARGUMENT, AKLR_ERR_UNSUPPORTED, AKLR_ERR_WORKSPACE, AKLR_ERR_LAUNCH = 1, 2, 3, 4
+AKLR_ERR_SCRATCH_LIMIT = 5
 FP8_E4M3FN, FP8_E5M2 = 0, 1
 OUT_BF16, OUT_F16 = 0, 1
 B_ROW_MAJOR, B_PRESHUFFLE_16x16 = 0, 1

@@ -181,28 +181,76 @@ __device__ __forceinline__ f32x4 load_partial4(rsrc_t r, int64_t elem) {
 }
 __host__ __device__ inline int64_t round4(int64_t m) { return (m + 3) / 4 * 4; }
 
-// Split-K arrival. Each workgroup of an output tile stores its fp32 partial with store_partial4,
-// then calls this (every thread of the workgroup): it waits until those stores are acknowledged,
-// bumps the tile's counter once with an agent-scope atomic, and returns true only in the workgroup
-// that arrives last. That one resets the counter to 0 for the next call and owns the reduction,
-// which it reads with load_partial4 and sums in split order, so the result does not depend on the
-// arrival order. `slot` is the workgroup's LDS word for the broadcast.
-__device__ __forceinline__ bool splitk_arrive(unsigned* counter, int splits, unsigned* slot) {
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are acknowledged
-  __syncthreads();                // ... and every other wave's
-  if (threadIdx.x == 0) *slot = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  const bool last = *slot == (unsigned)(splits - 1);
-  if (last && threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return last;
+// Split-K arrival words. One 64-bit word per output tile: bits 63..8 hold a tag of the launch, bits
+// 7..0 how many of the launch's workgroups of that tile have arrived. The tag is the dispatch packet's
+// id (its index in the HSA queue, new for every launch, graph replays included) xor a hash of the
+// queue's address (ids of two queues count from the same start), so a word whose tag is not this
+// launch's is a leftover of an earlier call, or garbage, and counts as zero arrivals. No call depends
+// on what the workspace held before it; calls that may run at the same time need their own workspace.
+extern "C" __device__ uint64_t aklr_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+constexpr uint64_t kTagMask = ~(uint64_t)0xFF;
+__device__ __forceinline__ uint64_t launch_tag() {
+  const uint64_t q = (uint64_t)(uintptr_t)__builtin_amdgcn_queue_ptr();
+  return (aklr_dispatch_id() ^ ((q * 0x9E3779B97F4A7C15ull) >> 8)) << 8;
 }
 
-// Workspace layout of the split-K GEMMs: a fixed 64 KiB region of counters, one per output tile
-// (at most 16384: n / 16 column groups for n <= 262144, or <= 512 tiles), zero before first use
-// and left zero by every call; then fp32 partials [splits, n, round4(m)]. The region's size is the same for
-// every call, so one call's partials never land on another's counters.
-constexpr size_t kSplitkCounterBytes = 65536;
-constexpr int64_t kSplitkMaxTiles = (int64_t)(kSplitkCounterBytes / 4);
+// The tile's word as the kernel starts, read by the thread that will arrive for its workgroup (before
+// that wave's other global loads, so it returns first). It is only a guess of the word's content:
+// splitk_arrive claims the word with a compare-and-swap against it, issued beside the partial
+// stores, and falls back to the value the swap returns.
+__device__ __forceinline__ uint64_t splitk_peek(const uint64_t* word) {
+  return __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Split-K arrival. Each workgroup of an output tile stores its fp32 partial with store_partial4,
+// then calls this (every thread of the workgroup). Thread `arriver` first claims the tile's word
+// for this launch -- a stale word becomes (tag, 0) by a compare-and-swap, which fails harmlessly
+// when another workgroup of the launch got there first -- in flight together with the partial
+// stores; once those are acknowledged it adds one arrival, and the workgroup that brings the count
+// to `splits` returns true. That one owns the reduction, which it reads with load_partial4 and sums
+// in split order, so the result does not depend on the arrival order. Nothing is reset: the next
+// launch's tag differs. `seen` is splitk_peek's value (meaningful in the arriver only); `slot` is
+// the workgroup's LDS word for the broadcast.
+__device__ __forceinline__ bool splitk_arrive(uint64_t* word, uint64_t seen, int splits, unsigned* slot,
+                                              unsigned arriver = 0) {
+  const uint64_t tag = launch_tag();
+  uint64_t cur = seen;
+  bool claimed = (seen & kTagMask) == tag;
+  if (threadIdx.x == arriver && !claimed)
+    claimed = __hip_atomic_compare_exchange_strong(word, &cur, tag, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores (and the claim) are acknowledged
+  __syncthreads();                // ... and every other wave's
+  if (threadIdx.x == arriver) {
+    // a failed swap returned the word: tagged by this launch, unless the peek was older than a value
+    // no workgroup of this launch wrote (then claim again from what the swap returned). Every failed
+    // swap means another workgroup's swap or add succeeded, and there are finitely many of those;
+    // the bound only keeps a misuse (two launches sharing a workspace at once) from spinning.
+    for (int i = 0; i < 64 && !claimed && (cur & kTagMask) != tag; ++i)
+      claimed = __hip_atomic_compare_exchange_strong(word, &cur, tag, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t old = __hip_atomic_fetch_add(word, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *slot = (unsigned)(old & 0xFF);
+  }
+  __syncthreads();
+  return *slot == (unsigned)(splits - 1);
+}
+
+// Workspace layout of the split-K GEMMs: a fixed 128 KiB region of arrival words, one per output tile
+// (at most 16384: n / 16 column groups for n <= 262144, or <= 512 tiles; no initial content needed),
+// then fp32 partials, each written by this call before any workgroup reads it. The region's size is
+// the same for every call, so one call's partials never land on another's words.
+constexpr size_t kSplitkCounterBytes = 131072;
+constexpr int64_t kSplitkMaxTiles = (int64_t)(kSplitkCounterBytes / 8);
+constexpr int kSplitkMaxSplits = 255;  // the count field's range
+
+// The FP8 GEMM entry (gemm_a8w8.hip) behind aklr_gemm_a8w8_blockscale: the caller's workspace of
+// workspace_bytes, or, when scratch_cap is nonzero, the device buffer `scratch` of scratch_cap bytes
+// (a plan that needs more returns AKLR_ERR_SCRATCH_LIMIT and launches nothing).
+int gemm8_entry(const void* a, int64_t lda, const void* b, int64_t ldb, const float* a_scale, int64_t sa_stride_m,
+                int64_t sa_stride_k, const float* b_scale, int64_t ldbs, const float* bias, void* out, int64_t ldo,
+                int64_t m, int64_t n, int64_t k, int fp8_dtype, int b_layout, int out_dtype, void* workspace,
+                size_t workspace_bytes, void* scratch, size_t scratch_cap, hipStream_t stream);
 
 }  // namespace aklr
 

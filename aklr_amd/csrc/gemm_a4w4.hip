@@ -37,7 +37,7 @@ struct Gemm4Args {
   int b_pre, scale_shuffled, out_dtype;
   int64_t pc;  // padded scale columns (shuffled layout)
   float* partial;
-  unsigned* counters;  // lds kernel split-K arrival counters
+  uint64_t* counters;  // split-K arrival words, one per output tile (launch-tagged)
   int splits;
   int ks_per_split;  // K steps per split: 128 values (decode), 256 values (lds)
   int pr_a, pr_b;    // padded scale rows (shuffled layout)
@@ -102,6 +102,9 @@ __global__ __launch_bounds__(NW * 64) void gemm4_skinny_kernel(Gemm4Args p) {
   const int64_t kbytes = p.k >> 1, kt32 = kbytes >> 5;
   const int kcols = p.k >> 5;  // scale columns
   const int64_t c8 = p.pc >> 3;
+  // split-K: thread 0 arrives for the workgroup; its peek of the arrival word returns first
+  uint64_t seen = 0;
+  if (p.splits > 1 && w == 0) seen = splitk_peek(p.counters + blockIdx.x);
 
   rsrc_t brs[NT];
   int64_t bcol[NT];
@@ -221,7 +224,7 @@ __global__ __launch_bounds__(NW * 64) void gemm4_skinny_kernel(Gemm4Args p) {
       if (row0 + r < p.m) store_out(p.out, (int64_t)(row0 + r) * p.ldo + col, sv[r] + bv, p.out_dtype);
   }
   if (p.splits == 1) return;
-  if (!splitk_arrive(p.counters + blockIdx.x, p.splits, &arrive_slot)) return;
+  if (!splitk_arrive(p.counters + blockIdx.x, seen, p.splits, &arrive_slot)) return;
   for (int t = w; t < T; t += NW) {
     const int mt = t / NT, nt = t % NT;
     const int c0 = n0 + nt * 16;
@@ -285,9 +288,14 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm4_stream_kernel(Gemm4Args p
   const int col_w = c0w + 4 * g;
   const int64_t plane = (int64_t)gridDim.x * NW * MT * NT * 256;  // split-K partials, accumulator order
   const int64_t part_base = ((int64_t)blockIdx.x * NW + w) * (MT * NT) * 256 + lane * 4;
+  // the loader's lane 0 arrives for the workgroup (split-K); its peek of the arrival word goes out
+  // before the stage loads, so it returns first
+  constexpr unsigned kArriver = NW * 64;
+  uint64_t seen = 0;
 
   if (w == NW) {
     // Loader. Rows past m and byte granules past k read the out-of-range offset (zeros).
+    if (p.splits > 1) seen = splitk_peek(p.counters + blockIdx.x);
     const i32x4 ars = make_rsrc_words(p.a, rsrc_bytes((int64_t)(p.m - 1) * p.lda + kbytes));
     const i32x4 sars = SSHUF ? make_rsrc_words(p.sa, rsrc_bytes((int64_t)p.pr_a * p.pc))
                              : make_rsrc_words(p.sa, rsrc_bytes((int64_t)(p.m - 1) * p.lds_a + kcols));
@@ -437,7 +445,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm4_stream_kernel(Gemm4Args p
   }
 
   if (p.splits > 1) {
-    if (!splitk_arrive(p.counters + blockIdx.x, p.splits, &arrive_slot)) return;
+    if (!splitk_arrive(p.counters + blockIdx.x, seen, p.splits, &arrive_slot, kArriver)) return;
     if (w == NW) return;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -665,6 +673,10 @@ __global__ __launch_bounds__(512) void gemm4_lds_kernel(Gemm4Args p) {
   const int ks_begin = split * p.ks_per_split;
   const int ks_end = min(KS, ks_begin + p.ks_per_split);
   const int64_t kbytes = p.k >> 1, kt32 = kbytes >> 5;
+  // split-K: thread 0 arrives for the workgroup; its peek of the arrival word goes out before the
+  // stage loads, so it returns first
+  uint64_t seen = 0;
+  if (p.splits > 1 && w == 0) seen = splitk_peek(p.counters + pid);
 
   auto clamp_bytes = [](int64_t b) { return (uint32_t)(b > 0x7FFFFFFFll ? 0x7FFFFFFFll : (b < 0 ? 0 : b)); };
   const i32x4 ars = make_rsrc_words(p.a + (int64_t)m0 * p.lda, clamp_bytes((int64_t)(p.m - 1 - m0) * p.lda + kbytes));
@@ -797,7 +809,7 @@ __global__ __launch_bounds__(512) void gemm4_lds_kernel(Gemm4Args p) {
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) store_partial4(prs, part_base + (mt * NT + nt) * 256, acc[mt][nt]);
-    if (!splitk_arrive(p.counters + pid, p.splits, &arrive_slot)) return;
+    if (!splitk_arrive(p.counters + pid, seen, p.splits, &arrive_slot)) return;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -992,7 +1004,7 @@ static void launch_lds4(const Gemm4Args& g, const Lds4Plan& p, hipStream_t s) {
 
 using namespace aklr;
 
-// Workspace: kSplitkCounterBytes of arrival counters, then fp32 partials: [splits, n, round4(m)] for
+// Workspace: kSplitkCounterBytes of arrival words, then fp32 partials: [splits, n, round4(m)] for
 // the skinny kernel, whole workgroup tiles for the LDS kernel. The LDS kernel may be declined at call
 // time (row-major scales with unaligned rows); the tile kernel that runs instead does not split K.
 static size_t lds4_partial_bytes(const Lds4Plan& p) {
@@ -1066,7 +1078,7 @@ extern "C" int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t
     if (sp.splits > 1) {
       const size_t need = kSplitkCounterBytes + stream4_partial_bytes(sp);
       if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) return AKLR_ERR_WORKSPACE;
-      g.counters = static_cast<unsigned*>(workspace);
+      g.counters = static_cast<uint64_t*>(workspace);
       g.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kSplitkCounterBytes);
     }
     const bool sshuf = scale_layout == AKLR_SCALES_SHUFFLED;
@@ -1082,7 +1094,7 @@ extern "C" int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t
     if (d.splits > 1) {
       const size_t need = kSplitkCounterBytes + (size_t)d.splits * (size_t)round4(m) * (size_t)n * sizeof(float);
       if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) return AKLR_ERR_WORKSPACE;
-      g.counters = static_cast<unsigned*>(workspace);
+      g.counters = static_cast<uint64_t*>(workspace);
       g.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kSplitkCounterBytes);
     }
     const bool sshuf = scale_layout == AKLR_SCALES_SHUFFLED;
@@ -1098,7 +1110,7 @@ extern "C" int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t
     if (lp.splits > 1) {
       const size_t need = kSplitkCounterBytes + lds4_partial_bytes(lp);
       if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) return AKLR_ERR_WORKSPACE;
-      g.counters = static_cast<unsigned*>(workspace);
+      g.counters = static_cast<uint64_t*>(workspace);
       g.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kSplitkCounterBytes);
     }
     const bool sshuf = scale_layout == AKLR_SCALES_SHUFFLED;

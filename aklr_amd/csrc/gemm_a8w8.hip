@@ -14,9 +14,9 @@
 //   row), a_scale staged in LDS, XCD-aware tile order, 16-byte output stores.
 //
 // When K is also split across workgroups, each stores an fp32 partial into the caller's workspace
-// and the last workgroup of the output tile to arrive (an agent-scope counter) sums the partials in
-// split order and writes the output: one launch, and every sum has a fixed order, so results are
-// bitwise reproducible.
+// and the last workgroup of the output tile to arrive (a launch-tagged agent-scope counter, valid
+// whatever the workspace held before) sums the partials in split order and writes the output: one
+// launch, and every sum has a fixed order, so results are bitwise reproducible.
 #include "common.h"
 
 namespace aklr {
@@ -35,7 +35,7 @@ struct Gemm8Args {
   int64_t ldo;
   int m, n, k;
   int out_dtype;
-  unsigned* counters;  // one per output tile when splits > 1
+  uint64_t* counters;  // when splits > 1: one arrival word per output tile (launch-tagged)
   float* partial;      // when splits > 1: per 16x16 tile, in accumulator order
   int splits;
   int kb_per_split;
@@ -99,6 +99,9 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * kCols;
+  // the loader's lane 0 arrives for the workgroup (split-K): it has no accumulators to keep in registers
+  constexpr unsigned kArriver = NW * 64;
+  uint64_t seen = 0;
   const int split = blockIdx.y;
   const int KB = p.k >> 7;
   const int kb_begin = split * p.kb_per_split;
@@ -121,6 +124,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   if (QA && w == NW) {
     // Fused quantization: the compute waves fill the A stages; the loader stages b_scale and keeps
     // the barrier count.
+    if (p.splits > 1) seen = splitk_peek(p.counters + blockIdx.x);
     const int len = kb_end - kb_begin;
     const int last_row = (p.n - 1) >> 7;
     for (int i = lane; i < kNBlk * len; i += 64) {
@@ -130,7 +134,9 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     stage_barrier();
     for (int kb = kb_begin; kb < kb_end; ++kb) stage_barrier();
   } else if (w == NW) {
-    // Loader. Rows past m read the out-of-range offset: zeros, no memory access.
+    // Loader. Rows past m read the out-of-range offset: zeros, no memory access. The arrival word's
+    // peek goes out first, so it has returned by the first full wait below.
+    if (p.splits > 1) seen = splitk_peek(p.counters + blockIdx.x);
     const i32x4 ars = make_rsrc_words(p.a, rsrc_bytes((int64_t)(p.m - 1) * p.lda + p.k));
     const i32x4 sars =
         make_rsrc_words(p.sa, rsrc_bytes(((int64_t)(p.m - 1) * p.sa_sm + (int64_t)(KB - 1) * p.sa_sk + 1) * 4));
@@ -392,7 +398,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   }
 
   if (p.splits > 1) {
-    if (!splitk_arrive(p.counters + blockIdx.x, p.splits, &arrive_slot)) return;
+    if (!splitk_arrive(p.counters + blockIdx.x, seen, p.splits, &arrive_slot, kArriver)) return;
     if (w == NW) return;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -545,6 +551,10 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   const int kb_begin = split * p.kb_per_split;
   const int kb_end = min(KB, kb_begin + p.kb_per_split);
   const int64_t kt32 = p.k >> 5;
+  // split-K: thread 0 arrives for the workgroup; its peek of the arrival word goes out before the
+  // stage loads, so it returns first
+  uint64_t seen = 0;
+  if (p.splits > 1 && w == 0) seen = splitk_peek(p.counters + pid);
 
   // Wave w moves rows [w*TM/8, (w+1)*TM/8) of the A tile and its BI slabs of the B tile, in slabs of 8
   // rows; waves below kScaleWaves move a_scale rows [64w, 64w + 64), the others issue an empty load so
@@ -680,7 +690,7 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) store_partial4(prs, part_base + (mt * NT + nt) * 256, acc[mt][nt]);
-    if (!splitk_arrive(p.counters + pid, p.splits, &arrive_slot)) return;
+    if (!splitk_arrive(p.counters + pid, seen, p.splits, &arrive_slot)) return;
     // Sum in split order, with all MT * NT loads of a batch of splits in flight together.
     uint32_t poff[MT][NT];
 #pragma unroll
@@ -782,7 +792,9 @@ struct Plan8 {
 };
 
 static void finish_splits(Plan8& p, int64_t KB, int64_t s) {
-  if (s < 1 || p.grid_x > kSplitkMaxTiles) s = 1;  // one counter per output tile must fit the region
+  // one arrival word per output tile must fit the region, and the count field the splits
+  if (s < 1 || p.grid_x > kSplitkMaxTiles) s = 1;
+  if (s > kSplitkMaxSplits) s = kSplitkMaxSplits;
   p.kb_per_split = (int)((KB + s - 1) / s);
   p.splits = (int)((KB + p.kb_per_split - 1) / p.kb_per_split);
 }
@@ -942,8 +954,8 @@ static void dispatch_stream_qa(const Gemm8Args& a, const Plan8& d, hipStream_t s
 
 // Workspace of the fused entry point: the GEMM's split-K workspace, then (unfused plans) the codes
 // [m, k] and group-major scales [k/128, m] of the quantized activations, each 256-byte aligned. The
-// codes start past the counter region even when the GEMM runs unsplit: a workspace is shared by
-// calls whose counters must stay zero.
+// codes start past the arrival-word region even when the GEMM runs unsplit, so the region's place is
+// the same in every workspace.
 static size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
 static size_t quant_codes_offset(const Plan8& p) {
   const size_t gemm = up256(workspace8(p));
@@ -986,12 +998,14 @@ extern "C" size_t aklr_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n
   return workspace8(plan8(m, n, k));
 }
 
-extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void* b, int64_t ldb,
-                                         const float* a_scale, int64_t sa_stride_m, int64_t sa_stride_k,
-                                         const float* b_scale, int64_t ldbs, const float* bias, void* out,
-                                         int64_t ldo, int64_t m, int64_t n, int64_t k, int fp8_dtype, int b_layout,
-                                         int out_dtype, void* workspace, size_t workspace_bytes,
-                                         hipStream_t stream) {
+// The FP8 GEMM with the scratch it needs taken from `workspace` (the caller's buffer of
+// workspace_bytes), or, when scratch_cap is nonzero, from the device buffer `scratch` of scratch_cap
+// bytes (a plan needing more returns AKLR_ERR_SCRATCH_LIMIT).
+int aklr::gemm8_entry(const void* a, int64_t lda, const void* b, int64_t ldb, const float* a_scale,
+                       int64_t sa_stride_m, int64_t sa_stride_k, const float* b_scale, int64_t ldbs,
+                       const float* bias, void* out, int64_t ldo, int64_t m, int64_t n, int64_t k, int fp8_dtype,
+                       int b_layout, int out_dtype, void* workspace, size_t workspace_bytes, void* scratch,
+                       size_t scratch_cap, hipStream_t stream) {
   if (!a || !b || !a_scale || !b_scale || !out) return AKLR_ERR_INVALID_ARGUMENT;
   if (m < 0 || n <= 0 || k <= 0 || k % 128 != 0 || n % 16 != 0) return AKLR_ERR_INVALID_ARGUMENT;
   if (m > (1 << 20) || n > 262144 || k > 65536) return AKLR_ERR_INVALID_ARGUMENT;
@@ -1037,8 +1051,13 @@ extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void*
   g.kb_per_split = plan.kb_per_split;
   if (plan.splits > 1) {
     const size_t need = workspace8(plan);
-    if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) return AKLR_ERR_WORKSPACE;
-    g.counters = static_cast<unsigned*>(workspace);
+    if (scratch_cap) {
+      if (need > scratch_cap) return AKLR_ERR_SCRATCH_LIMIT;
+      workspace = scratch;
+    } else if (!workspace || workspace_bytes < need || !aklr_aligned16(workspace)) {
+      return AKLR_ERR_WORKSPACE;
+    }
+    g.counters = static_cast<uint64_t*>(workspace);
     g.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kSplitkCounterBytes);
   }
   if (plan.kind == Kernel8::kStream) {
@@ -1050,6 +1069,16 @@ extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void*
   }
   AKLR_LAUNCH_CHECK();
   return AKLR_OK;
+}
+
+extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void* b, int64_t ldb,
+                                         const float* a_scale, int64_t sa_stride_m, int64_t sa_stride_k,
+                                         const float* b_scale, int64_t ldbs, const float* bias, void* out,
+                                         int64_t ldo, int64_t m, int64_t n, int64_t k, int fp8_dtype, int b_layout,
+                                         int out_dtype, void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream) {
+  return gemm8_entry(a, lda, b, ldb, a_scale, sa_stride_m, sa_stride_k, b_scale, ldbs, bias, out, ldo, m, n, k,
+                     fp8_dtype, b_layout, out_dtype, workspace, workspace_bytes, nullptr, 0, stream);
 }
 
 extern "C" size_t aklr_quant_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k) {
@@ -1117,7 +1146,7 @@ extern "C" int aklr_quant_gemm_a8w8_blockscale(const void* x, int64_t ldx, const
   g.splits = plan.splits;
   g.kb_per_split = plan.kb_per_split;
   if (plan.splits > 1) {
-    g.counters = reinterpret_cast<unsigned*>(ws);
+    g.counters = reinterpret_cast<uint64_t*>(ws);
     g.partial = reinterpret_cast<float*>(ws + kSplitkCounterBytes);
   }
   if (b_layout == AKLR_B_PRESHUFFLE_16x16) dispatch_stream_qa<true>(g, plan, stream);

@@ -240,6 +240,7 @@ extern "C" const char* aklr_status_string(int status) {
     case AKLR_ERR_UNSUPPORTED: return "unsupported layout or dtype";
     case AKLR_ERR_WORKSPACE: return "workspace too small";
     case AKLR_ERR_LAUNCH: return "kernel launch failed";
+    case AKLR_ERR_SCRATCH_LIMIT: return "needs more scratch than the no-allocation entry point holds";
     default: return "unknown status";
   }
 }

@@ -15,10 +15,10 @@ Mirrors aklr/core/runtime/dispatch/_dispatcher.py:
   process (aklr/core/runtime/dispatch/_trace.py:36-100).
 
 What differs by design: there is no per-shape dispatch table. Every in-contract call that reaches a
-supported layout is served by the compiled HIP kernels; nothing compiles at call time. The one warm-up
-is a GEMM's split-K workspace (``aklr_amd.workspace``): a call first met inside a graph capture that
-would have to allocate it returns ``NOT_WARMED``. Layouts the kernels do not implement return
-``NO_WORKLOAD``. A kernel that fails raises; it does not fall back (_dispatcher.py:217-229).
+supported layout is served by the compiled HIP kernels; nothing compiles at call time, so a call first
+met inside a graph capture is served too (its split-K scratch is a per-call ``torch.empty``, which a
+capture takes from the graph's pool; ``aklr_amd.workspace``). Layouts the kernels do not implement
+return ``NO_WORKLOAD``. A kernel that fails raises; it does not fall back (_dispatcher.py:217-229).
 """
 from __future__ import annotations
 

@@ -182,8 +182,6 @@ def gemm_a8w8_blockwise_scaled(
         return _OOC
     if not trans_b:
         return FallbackReason.NO_WORKLOAD
-    if not workspace.ready(a.device, _lib.lib().aklr_gemm_a8w8_blockscale_workspace_bytes(m, n, k)):
-        return FallbackReason.NOT_WARMED
     b_layout = _lib.B_ROW_MAJOR if variant == "row_major" else _lib.B_PRESHUFFLE_16x16
     path = "stream" if m <= 128 else "lds"  # the library picks the same way (kStreamMaxM)
     return _Gemm8Plan(a, b, a_scale, b_scale, bias, out, dt, m, n, k, sa_sm, sa_sk, b_layout, variant,
@@ -266,8 +264,6 @@ def quant_gemm_a8w8_blockwise_scaled(x, b, b_scale, bias=None, out_dtype=None, o
         return _OOC
     if not _out_ok(out, m, n, dt, x.device, (x, b, b_scale, bias)):
         return _OOC
-    if not workspace.ready(x.device, _lib.lib().aklr_quant_gemm_a8w8_blockscale_workspace_bytes(m, n, k)):
-        return FallbackReason.NOT_WARMED
     fused = _lib.lib().aklr_quant_gemm_a8w8_blockscale_fused(m, n, k) == 1  # as the library picks
     path = "stream_fused" if fused else ("stream" if m <= 128 else "lds")
     return _QuantGemm8Plan(x, b, b_scale, bias, out, dt, m, n, k, b_layout, variant,
@@ -377,8 +373,6 @@ def gemm_a4w4_mxfp4(
         return _OOC
     if not _out_ok(out, m, n, dt, a.device, (a, b, a_scale, b_scale, bias)):
         return _OOC
-    if not workspace.ready(a.device, _lib.lib().aklr_gemm_a4w4_mxfp4_workspace_bytes(m, n, k)):
-        return FallbackReason.NOT_WARMED
     pre = variant == "b_shuffled"
     path = "skinny" if m <= 16 else ("stream" if m <= 32 else "lds")  # as the library picks (aligned scales)
     return _Gemm4Plan(a, b, a_scale, b_scale, bias, out, dt, m, n, k,

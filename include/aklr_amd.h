@@ -7,10 +7,13 @@
  * Entry points are stateless and may be called from any host thread with its own stream.
  *
  * Scratch memory is brought by the caller: ask *_workspace_bytes() for the size and pass a device
- * buffer at least that large (16-byte aligned). Its first 64 KiB are split-K arrival counters: they
- * must be zero before the buffer's first use, and every call leaves them zero again, so one buffer
- * serves any sequence of calls on one stream (calls that may run concurrently need their own
- * buffers). The rest holds fp32 partials. The library keeps nothing between calls.
+ * buffer at least that large (16-byte aligned), with any content -- freshly allocated and never
+ * cleared is fine. Its first 128 KiB are split-K arrival words, each tagged with the launch that
+ * wrote it (the HSA dispatch id and queue), so a word left by an earlier call, or garbage, counts as
+ * empty; the rest holds fp32 partials that the call writes before it reads them. No call depends on
+ * what an earlier call left, as the reference's kernel ABI requires of scratch (aklr/ops/README.md:214).
+ * Calls that may run at the same time need their own buffers. The library keeps nothing between
+ * calls.
  *
  * Each entry point replaces one kernel ABI of the reference (a TORCH_LIBRARY `run(...)` op that
  * AKLR's HipBuilder loads); the citation is on each declaration.
@@ -35,7 +38,8 @@ enum {
     AKLR_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size, misaligned pointer or stride */
     AKLR_ERR_UNSUPPORTED = 2,      /* a layout/dtype combination no kernel here serves */
     AKLR_ERR_WORKSPACE = 3,        /* workspace smaller than *_workspace_bytes() */
-    AKLR_ERR_LAUNCH = 4            /* hipGetLastError() after the launch was not hipSuccess */
+    AKLR_ERR_LAUNCH = 4,           /* hipGetLastError() after the launch was not hipSuccess */
+    AKLR_ERR_SCRATCH_LIMIT = 5     /* the plan needs more scratch than a no-allocation entry holds */
 };
 
 /* Element types. */
@@ -121,7 +125,7 @@ int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void* b, int64_t
  *   quantize each K block into LDS); larger m runs the two kernels, the codes and scales in the workspace.
  * x: bf16 [m, k], row stride ldx elements (multiple of 8). b, b_scale, bias, out as in
  *   aklr_gemm_a8w8_blockscale. The workspace (aklr_quant_gemm_a8w8_blockscale_workspace_bytes) obeys
- *   the same rules (16-byte aligned, leading counters zero, left zero).
+ *   the same rules (16-byte aligned, any content).
  */
 size_t aklr_quant_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k);
 /* 1 when aklr_quant_gemm_a8w8_blockscale runs (m, n, k) as one launch, 0 when as the two kernels

@@ -74,9 +74,9 @@ def test_workspace_sizes_are_host_computable(native_lib):
     up = lambda x, q: -(-x // q) * q
     for m, n, k in ((1, 2112, 7168), (16, 7168, 16384), (4096, 7168, 16384), (128, 24576, 1536), (256, 2112, 7168)):
         ws = L.aklr_gemm_a8w8_blockscale_workspace_bytes(m, n, k)
-        # 64 KiB of split-K counters plus at most 8 splits of fp32 partials over whole 16x16 tiles of
-        # workgroups at most 256 x 256
-        assert ws % 1024 == 0 and ws <= 65536 + 8 * up(m, 256) * up(n, 256) * 4
+        # 128 KiB of split-K arrival words plus at most 8 splits of fp32 partials over whole 16x16 tiles
+        # of workgroups at most 256 x 256
+        assert ws % 1024 == 0 and ws <= 131072 + 8 * up(m, 256) * up(n, 256) * 4
     assert L.aklr_gemm_a4w4_mxfp4_workspace_bytes(1, 10240, 8192) % 4 == 0
 
 
@@ -89,6 +89,7 @@ def test_quant_gemm_path_and_workspace_are_host_computable(native_lib):
     assert fused(17, 7168, 16384) == 0 and fused(300, 1024, 2048) == 0
     assert fused(1, 4096, 8192) == 0
     assert fused(0, 7168, 16384) == 0 and fused(1, 7168, 64) == 0
-    # the two-kernel path stages the codes and scales past the 64 KiB counter region
+    # the two-kernel path stages the codes and scales past the 128 KiB arrival-word region
     m, n, k = 20, 2112, 128
-    assert L.aklr_quant_gemm_a8w8_blockscale_workspace_bytes(m, n, k) >= 65536 + m * k + (k // 128) * m * 4
+    assert L.aklr_quant_gemm_a8w8_blockscale_workspace_bytes(m, n, k) >= 131072 + m * k + (k // 128) * m * 4
+

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import aklr_amd
-from aklr_amd import layouts, workloads, workspace
+from aklr_amd import layouts, workloads
 from oracle import gemm as ogemm
 from oracle import quant as oquant
 from tests.helpers import bf16_bits, f32, say, u8
@@ -239,9 +239,6 @@ def test_quant_gemm_fused_matches_two_ops(m, n, k, shuffled, bias, fp16):
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), \
         f"fused quant+GEMM differs from the two ops: max|diff| {(got.float() - ref.float()).abs().max().item():.3e}"
-    # the shared workspace's split-K counters are zero again (the two-kernel path stages its codes past them)
-    ws = workspace.get(DEV, 1)
-    assert not ws[:65536].any(), "quant_gemm left non-zero split-K counters in the workspace"
     info = aklr_amd.quant_gemm_a8w8_blockwise_scaled.serving(x, b if not shuffled else bb, bs, bias=bias_t,
                                                               out_dtype=od,
                                                               operand_format="none:preshuffled" if shuffled else "none:none")
