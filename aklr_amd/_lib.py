@@ -30,6 +30,11 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_int, _c_int, _c_int, _vp, _c_size, _vp],
     ),
+    "aklr_gemm_a8w8_blockscale_noalloc": (
+        _c_int,
+        [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_int, _c_int, _c_int, _vp],
+    ),
     "aklr_quant_gemm_a8w8_blockscale_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "aklr_quant_gemm_a8w8_blockscale_fused": (_c_int, [_c_i64, _c_i64, _c_i64]),
     "aklr_quant_gemm_a8w8_blockscale": (
@@ -63,6 +68,7 @@ SIGNATURES: dict[str, tuple] = {
 AKLR_OK = 0
 AKLR_ERR_INVALID_ARGUMENT, AKLR_ERR_UNSUPPORTED, AKLR_ERR_WORKSPACE, AKLR_ERR_LAUNCH = 1, 2, 3, 4
 AKLR_ERR_SCRATCH_LIMIT = 5
+NOALLOC_SCRATCH_BYTES = 32 << 20  # AKLR_NOALLOC_SCRATCH_BYTES
 FP8_E4M3FN, FP8_E5M2 = 0, 1
 OUT_BF16, OUT_F16 = 0, 1
 B_ROW_MAJOR, B_PRESHUFFLE_16x16 = 0, 1

@@ -116,6 +116,25 @@ int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void* b, int64_t
                               size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * aklr_gemm_a8w8_blockscale without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture that must not call hipMalloc, tight serving loops, harnesses
+ * that forbid allocation). No counterpart in the reference: its kernels take scratch from torch
+ * allocations inside the call (aklr/ops/README.md:214).
+ * Same arguments, kernels, plans and results (bit for bit) as aklr_gemm_a8w8_blockscale. The split-K
+ * scratch is a device array of AKLR_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until
+ * the process ends; a plan that needs more (aklr_gemm_a8w8_blockscale_workspace_bytes() larger than
+ * that: only m > 128 with few output tiles) returns AKLR_ERR_SCRATCH_LIMIT and launches nothing. Every
+ * shape of the DeepSeek-V3 decode and prefill configurations fits. The entry point allocates nothing
+ * (it looks the array's address up once per device). Calls on one GPU share the array: calls that may
+ * overlap in time (other streams, other host threads) race.
+ */
+#define AKLR_NOALLOC_SCRATCH_BYTES (32u << 20)
+int aklr_gemm_a8w8_blockscale_noalloc(const void* a, int64_t lda, const void* b, int64_t ldb, const float* a_scale,
+                                      int64_t sa_stride_m, int64_t sa_stride_k, const float* b_scale, int64_t ldbs,
+                                      const float* bias, void* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
+                                      int fp8_dtype, int b_layout, int out_dtype, hipStream_t stream);
+
+/*
  * Per-1x128 FP8 quantization of bf16 activations fused into the block-scaled FP8 GEMM:
  * out = GEMM(per_group_quant_fp8(x), b), equal bit for bit to aklr_per_group_quant_fp8 followed by
  * aklr_gemm_a8w8_blockscale on its codes and group-major scales (e4m3fn).

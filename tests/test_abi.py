@@ -93,3 +93,15 @@ def test_quant_gemm_path_and_workspace_are_host_computable(native_lib):
     m, n, k = 20, 2112, 128
     assert L.aklr_quant_gemm_a8w8_blockscale_workspace_bytes(m, n, k) >= 131072 + m * k + (k // 128) * m * 4
 
+
+def test_every_plan_fits_the_noalloc_scratch(native_lib):
+    # aklr_gemm_a8w8_blockscale_noalloc serves a plan only when its workspace fits the library's scratch
+    # array; the planner splits K only while the workgroups stay about one round (<= 256), which bounds
+    # every plan's scratch below the array: a sweep over m, n, k finds none larger
+    L = native_lib
+    worst = 0
+    for m in (1, 4, 16, 17, 32, 64, 100, 128, 129, 200, 256, 300, 512, 1024, 2048, 4096, 8192, 2**20):
+        for n in (16, 48, 144, 1024, 1920, 2112, 4096, 7168, 24576, 65536, 262144):
+            for k in (128, 512, 2048, 7168, 16384, 65536):
+                worst = max(worst, L.aklr_gemm_a8w8_blockscale_workspace_bytes(m, n, k))
+    assert 0 < worst <= _lib.NOALLOC_SCRATCH_BYTES
