@@ -81,18 +81,38 @@ class _MoePlan:
     kernel_ref: str = field(default="aklr_deepseek_v2_fp8_moe:grouped")
 
 
+_I32_LIMIT = 0x7FFFFFFE  # the kernels' 32-bit byte offsets stay below 2 GiB
+
+
+def token_chunks(tokens: int, d: int, inter: int, slots: int) -> list[tuple[int, int]]:
+    """[start, end) token ranges one library call each can take. The kernels address the routed rows'
+    activations (R x D bf16), the intermediate h (R x I) and the input (T x D) with 32-bit offsets,
+    R = tokens x slots, so the library takes at most that many tokens per call (the limits of its
+    dims_ok); every token's output depends on that token alone (its routing, its rows through the
+    experts, its combine), so a larger call runs as consecutive calls on row ranges."""
+    most = min(65536, _I32_LIMIT // (2 * d * slots), _I32_LIMIT // (inter * slots), _I32_LIMIT // d)
+    if most < 1:
+        return []
+    return [(s, min(tokens, s + most)) for s in range(0, tokens, most)]
+
+
 def _run_moe(p: _MoePlan):
     dev = p.hidden.device
     out = torch.empty((p.tokens, p.d), dtype=torch.bfloat16, device=dev)
     L = _lib.lib()
-    ws_bytes = L.aklr_moe_fp8_workspace_bytes(p.tokens, p.d, p.inter, p.n_routed + 1, p.topk + 1, p.n_routed)
+    chunks = token_chunks(p.tokens, p.d, p.inter, p.topk + 1)
+    most = max(e - s for s, e in chunks)
+    ws_bytes = L.aklr_moe_fp8_workspace_bytes(most, p.d, p.inter, p.n_routed + 1, p.topk + 1, p.n_routed)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    st = L.aklr_deepseek_v2_fp8_moe(
-        p.hidden.data_ptr(), p.router_weight.data_ptr(), p.correction_bias.data_ptr(), p.w1.data_ptr(),
-        p.w1_scale.data_ptr(), p.w2.data_ptr(), p.w2_scale.data_ptr(), p.tokens, p.d, p.inter, p.n_routed, p.topk,
-        p.groups, p.topk_group, 1, p.scale, p.w_layout, out.data_ptr(), ws.data_ptr(), ws_bytes, _stream(dev),
-    )
-    _lib.check(st, "deepseek_v2_fp8_moe")
+    row = p.d * 2  # bytes per hidden / out row
+    for s, e in chunks:
+        st = L.aklr_deepseek_v2_fp8_moe(
+            p.hidden.data_ptr() + s * row, p.router_weight.data_ptr(), p.correction_bias.data_ptr(), p.w1.data_ptr(),
+            p.w1_scale.data_ptr(), p.w2.data_ptr(), p.w2_scale.data_ptr(), e - s, p.d, p.inter, p.n_routed, p.topk,
+            p.groups, p.topk_group, 1, p.scale, p.w_layout, out.data_ptr() + s * row, ws.data_ptr(), ws_bytes,
+            _stream(dev),
+        )
+        _lib.check(st, "deepseek_v2_fp8_moe")
     return out
 
 
@@ -204,15 +224,18 @@ def moe_fp8_experts(hidden_states, w1, w2, topk_weights, topk_ids, w1_scale, w2_
         raise ValueError("topk_ids and topk_weights must both be [T, slots]")
     slots = ids.shape[1]
     L = _lib.lib()
-    ws_bytes = L.aklr_moe_fp8_workspace_bytes(t, d, inter, e, slots, 0)
+    chunks = token_chunks(t, d, inter, slots)
+    ws_bytes = L.aklr_moe_fp8_workspace_bytes(max((b - a for a, b in chunks), default=0), d, inter, e, slots, 0)
     if ws_bytes == 0:
         raise ValueError("moe_fp8_experts: sizes outside what the kernels take")
     out = torch.empty((t, d), dtype=torch.bfloat16, device=hidden_states.device)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=hidden_states.device)
-    st = L.aklr_moe_fp8_experts(
-        hidden_states.data_ptr(), t, d, inter, e, ids.data_ptr(), weights.data_ptr(), slots, w1.data_ptr(),
-        w1_scale.data_ptr(), w2.data_ptr(), w2_scale.data_ptr(), layout[1], out.data_ptr(), ws.data_ptr(), ws_bytes,
-        _stream(hidden_states.device),
-    )
-    _lib.check(st, "moe_fp8_experts")
+    for a, b in chunks:
+        st = L.aklr_moe_fp8_experts(
+            hidden_states.data_ptr() + a * d * 2, b - a, d, inter, e, ids.data_ptr() + a * slots * 4,
+            weights.data_ptr() + a * slots * 4, slots, w1.data_ptr(), w1_scale.data_ptr(), w2.data_ptr(),
+            w2_scale.data_ptr(), layout[1], out.data_ptr() + a * d * 2, ws.data_ptr(), ws_bytes,
+            _stream(hidden_states.device),
+        )
+        _lib.check(st, "moe_fp8_experts")
     return out

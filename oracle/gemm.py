@@ -18,6 +18,8 @@ hand-worked bytes.
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 
 from .formats import e8m0_to_f32, fp4x2_to_f32, fp8_to_f32
@@ -100,3 +102,29 @@ def within_contract_tolerance(actual, expected, out_dtype="bfloat16") -> bool:
     expected = np.asarray(expected, dtype=np.float64)
     err = np.abs(np.asarray(actual, dtype=np.float64) - expected)
     return bool(np.all(err <= atol + (rtol + u) * np.abs(expected)))
+
+
+FP32_UNIT_ROUNDOFF = 2.0**-24
+OUT_UNIT_ROUNDOFF = {"bfloat16": 2.0**-8, "float16": 2.0**-11}
+
+
+def dot_product_bound(expected, magnitude, k: int, out_dtype="bfloat16", max_split_k=1) -> np.ndarray:
+    """DotProductBound (aklr/core/contract/semantics/_compare.py:338-356), the gemm_a4w4_mxfp4 contract's
+    error bound (aklr/ops/gemm/contract.py:375, max_split_k=1): per element
+    B = 2 (6 sqrt(n_eff) + 2) u_fp32 * M + u_out * |y|, where M is the reference computed on the
+    inputs' absolute values and n_eff = max over s <= max_split_k of ceil(k / s) + bit_length(s - 1)."""
+    n_eff = max(-(-k // s) + (s - 1).bit_length() for s in range(1, max_split_k + 1))
+    multiple = 6.0 * math.sqrt(n_eff) + 2.0
+    return (2.0 * multiple * FP32_UNIT_ROUNDOFF * np.abs(np.asarray(magnitude, dtype=np.float64))
+            + OUT_UNIT_ROUNDOFF[out_dtype] * np.abs(np.asarray(expected, dtype=np.float64)))
+
+
+def within_dot_product_bound(actual, expected, magnitude, k: int, out_dtype="bfloat16", max_split_k=1) -> bool:
+    """Every element within dot_product_bound (the gemm contracts compare with max_violation_fraction
+    0, aklr/core/contract/spec/_args.py:203) and the errors unbiased: |mean| / rms <= 5 / sqrt(n)
+    (ElementwiseBound's bias test, _compare.py:313-326)."""
+    err = np.asarray(actual, dtype=np.float64) - np.asarray(expected, dtype=np.float64)
+    if not np.all(np.abs(err) <= dot_product_bound(expected, magnitude, k, out_dtype, max_split_k)):
+        return False
+    rms = float(np.sqrt(np.mean(err * err))) if err.size else 0.0
+    return rms == 0.0 or abs(float(err.mean())) / rms <= 5.0 / math.sqrt(err.size)

@@ -2,7 +2,7 @@
 ``oracle/__init__.py``).
 
 Follows aklr/plugins/sglang/models/deepseek_v2/reference.py:
-- router logits: fp32 ``x @ router_weight^T`` rounded to bf16 (:169-170);
+- router logits: fp32 ``x @ router_weight^T`` rounded to bf16 (:173);
 - ``_grouped_routed`` (:121-143): scores = sigmoid(logits); biased = scores + correction_bias;
   experts fall into num_expert_group equal groups, a group scored by its two best biased scores
   summed; the topk_group best groups are kept (lower index first among equals, ``_first_largest``
@@ -27,7 +27,11 @@ scores (checked against an independent argpartition), the kept-group invariants 
 explicit ties (lower index first), weights from the unbiased scores (a bias that changes the picks
 but not the weights), the division-vs-multiply scale on values where the two differ in fp32,
 ``_fp8_linear`` reducing to the pinned a8w8 GEMM oracle, and the combine on one-expert and
-shared-only routings.
+shared-only routings. ``router_logits`` by products exact in fp32 that sit on bf16 ties (ties to even)
+and one whose fp32 rounding decides the bf16 value (so the product is rounded to fp32 first, as the
+reference's fp32 matmul is); the composed ``deepseek_v2_fp8_moe`` by reduction to ``moe_experts`` on a
+forced routing with hand-computed weights, and against a per-token loop that routes by repeated
+maximum in float64.
 """
 from __future__ import annotations
 

@@ -206,3 +206,23 @@ def test_moe_workspace_bytes(native_lib):
     r = 4096 * 9
     assert b >= r * 7168 * 2 + r * 2048 + 4096 * 7168
     assert native_lib.aklr_moe_fp8_workspace_bytes(4096, 7000, 2048, 257, 9, 256) == 0
+
+
+def test_moe_large_token_counts_are_served_in_chunks(moe_as_gpu, native_lib):
+    # In contract up to 65536 tokens; the kernels' 32-bit offsets take fewer per call at D=7168 (9 slots:
+    # R * D * 2 < 2**31 -> 16644 tokens). serving() says served, and the host runs the call as chunks the
+    # library takes, each with a workspace it sizes (so the call cannot raise for its size).
+    from aklr_amd import moe as hm
+
+    d, inter, slots = 7168, 2048, 9
+    for tokens in (1, 4096, 16644, 16645, 32768, 65536):
+        chunks = hm.token_chunks(tokens, d, inter, slots)
+        assert chunks[0][0] == 0 and chunks[-1][1] == tokens
+        assert all(a < b and b == c for (a, b), (c, _) in zip(chunks, chunks[1:] + [(tokens, 0)]))
+        for a, b in chunks:
+            assert native_lib.aklr_moe_fp8_workspace_bytes(b - a, d, inter, 257, slots, 256) > 0
+        assert len(chunks) == -(-tokens // 16644)
+    # the largest chunk is the library's own limit: one more token is refused
+    assert native_lib.aklr_moe_fp8_workspace_bytes(16645, d, inter, 257, slots, 256) == 0
+    args = _moe_args(t=32768, n_routed=16, d=7168, inter=128)
+    assert not isinstance(aklr_amd.deepseek_v2_fp8_moe.serving(*args), FR)

@@ -318,7 +318,15 @@ def _mxfp4_run(m, n, k, shuffled, seed=0, rows=64, cols=512, bias=False):
     r, c = _sample(m, n, rows, cols, seed)
     ref = ogemm.gemm_a4w4_mxfp4(u8(qa_rm), u8(wb), u8(sa_rm), u8(sb), bias=None if bias_t is None else f32(bias_t),
                                 rows=r, cols=c)
-    _check(f32(out)[np.ix_(r, c)], ref, f"mxfp4 m={m} n={n} k={k}", contract=False)
+    got = f32(out)[np.ix_(r, c)]
+    _check(got, ref, f"mxfp4 m={m} n={n} k={k}", contract=False)
+    # the contract's own bound, DotProductBound(max_split_k=1) (aklr/ops/gemm/contract.py:375): M is the
+    # product of the operands' absolute values (sign bits cleared, as the reference's absolute_value does)
+    mag = ogemm.gemm_a4w4_mxfp4(u8(qa_rm) & 0x77, u8(wb) & 0x77, u8(sa_rm), u8(sb),
+                                bias=None if bias_t is None else np.abs(f32(bias_t)), rows=r, cols=c)
+    peak = float(np.max(np.abs(got - ref) / ogemm.dot_product_bound(ref, mag, k)))
+    say(f"  DotProductBound peak multiple {peak:.3f}")
+    assert ogemm.within_dot_product_bound(got, ref, mag, k), f"mxfp4 m={m} n={n} k={k}: DotProductBound exceeded"
     return out
 
 
@@ -369,3 +377,21 @@ def test_workspace_shared_across_shapes():
               (1, 24576, 1536)]
     for i, (m, n, k) in enumerate(shapes):
         _run_and_check(m, n, k, variant="b_shuffled", rows=128, cols=2048, seed=60 + i)
+
+
+@pytest.mark.parametrize("nk", workloads.DEEPSEEK_NK)
+@pytest.mark.parametrize("m", workloads.DECODE_M)
+def test_quant_gemm_fused_against_the_oracle(m, nk):
+    # quant_gemm_a8w8_blockwise_scaled (one launch at m <= 16) straight against the oracle, which quantizes
+    # the same bf16 input itself (aklr/ops/quant/reference.py:9-28, then aklr/ops/gemm/reference.py:90-105)
+    n, k = nk
+    say(f"quant_gemm vs oracle m={m} n={n} k={k}")
+    x = workloads.activations(m, k, seed=90 + m, device=DEV)
+    b, bs = workloads.blockwise_fp8_weight(n, k, seed=91, device=DEV)
+    out = aklr_amd.quant_gemm_a8w8_blockwise_scaled(x, layouts.shuffle_weight(b), bs, operand_format="none:preshuffled")
+    assert isinstance(out, torch.Tensor), out
+    torch.cuda.synchronize()
+    r, c = _sample(m, n, 128, 1024, seed=m)
+    q_ref, s_ref = oquant.per_group_quant_fp8(bf16_bits(x))
+    ref = ogemm.gemm_a8w8_blockwise_scaled(q_ref, u8(b), s_ref, bs.cpu().numpy(), scale_major_mode="MN", rows=r, cols=c)
+    _check(f32(out)[np.ix_(r, c)], ref, f"quant_gemm m={m} n={n} k={k}")

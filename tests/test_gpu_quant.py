@@ -107,6 +107,32 @@ def test_mxfp4(m, k, shuffle):
     assert_same_bits(u8(s), s_ref, "mxfp4 scales")
 
 
+def test_mxfp4_every_bf16_value_through_unit_scale():
+    # A 32-value block whose amax is 6.0 gets E = 0 (frexp(6) = (0.75, 3): 3 - 3 + (0.75 > 0.75) = 0), a
+    # unit scale, so each value is rounded to e2m1 as it is: every finite bf16 value of magnitude <= 6
+    # (both signs, zeros and subnormals included) goes through the kernel's conversion once and must
+    # give the oracle's nibble (midpoints to the even code, sign kept).
+    bits = np.arange(0, 0x40C1, dtype=np.uint16)  # +0 .. 6.0
+    assert ofmt.bf16_bits_to_f32(np.array([0x40C0], np.uint16))[0] == 6.0
+    allbits = np.concatenate([bits, bits | 0x8000])
+    per_block = 31
+    blocks = -(-allbits.size // per_block)
+    rows = -(-blocks // 32)  # 32 blocks per row of 1024 values
+    data = np.zeros((rows * 32, 32), dtype=np.uint16)
+    data[:, 0] = 0x40C0  # 6.0 in every block
+    flat = np.zeros(rows * 32 * per_block, dtype=np.uint16)
+    flat[: allbits.size] = allbits
+    data[:, 1:] = flat.reshape(rows * 32, per_block)
+    x = torch.from_numpy(data.reshape(rows, 1024).view(np.int16)).view(torch.bfloat16).to(DEV)
+    say(f"dynamic_mxfp4_quant every bf16 |v| <= 6: {allbits.size} values in {rows} rows")
+    q, s = aklr_amd.dynamic_mxfp4_quant(x)
+    torch.cuda.synchronize()
+    q_ref, s_ref = oquant.dynamic_mxfp4_quant(data.reshape(rows, 1024))
+    assert np.all(s_ref == 127)
+    assert_same_bits(u8(s), s_ref, "mxfp4 unit scales")
+    assert_same_bits(u8(q), q_ref, "mxfp4 codes of every bf16 value")
+
+
 def test_mxfp4_matches_weight_quantizer():
     # the torch weight quantizer of aklr_amd.workloads and the GPU activation kernel implement the same rule
     x = workloads.activations(64, 4096, seed=11, device=DEV)

@@ -116,3 +116,24 @@ def test_tolerance_checks_reject_planted_error():
     assert not g.within_contract_tolerance(bad, y)
     near = y * (1 + 2.0**-9)  # inside one bf16 rounding
     assert g.within_north_star(near, y) and g.within_contract_tolerance(near, y)
+
+
+def test_dot_product_bound():
+    # B = 2 (6 sqrt(k) + 2) 2**-24 M + 2**-8 |y| (the reference's DotProductBound, max_split_k 1);
+    # k = 64 gives 100 * 2**-24 * M
+    y = np.array([1.0, -2.0, 0.5, 3.0])
+    mag = np.array([4.0, 4.0, 1.0, 8.0])
+    b = g.dot_product_bound(y, mag, 64)
+    np.testing.assert_allclose(b, 100 * 2.0**-24 * mag + 2.0**-8 * np.abs(y), rtol=1e-12)
+    # splitting K never lengthens the effective reduction: k stays the largest term
+    assert np.array_equal(g.dot_product_bound(y, mag, 8192, max_split_k=16), g.dot_product_bound(y, mag, 8192))
+    rng = np.random.default_rng(0)
+    y = rng.normal(size=4096)
+    mag = np.abs(y) * 3 + 1
+    bound = g.dot_product_bound(y, mag, 1024)
+    sign = rng.choice([-1.0, 1.0], size=y.size)
+    assert g.within_dot_product_bound(y + 0.5 * bound * sign, y, mag, 1024)  # inside, unbiased
+    bad = y + 0.5 * bound * sign
+    bad[17] = y[17] + 1.5 * bound[17]
+    assert not g.within_dot_product_bound(bad, y, mag, 1024)  # one element outside
+    assert not g.within_dot_product_bound(y + 0.5 * bound, y, mag, 1024)  # inside, but all one sign

@@ -144,3 +144,99 @@ def test_sqnr_db():
     ref = np.ones(100)
     assert moe.sqnr_db(ref, ref) == float("inf")
     assert abs(moe.sqnr_db(ref, ref * 1.01) - 40.0) < 1e-6
+
+
+def test_router_logits_round_the_fp32_product_to_bf16():
+    # deepseek_v2/reference.py:173: rounded_to_bfloat16(x @ router_weight^T), the product in fp32.
+    # Rows 0-2 are products exact in fp32 that sit on bf16 ties (ties to the even mantissa: 1 + 2**-8 ->
+    # 1.0, 1 + 3 * 2**-8 -> 1 + 2**-6; a truncation, a round-half-up or a skipped rounding fails one).
+    # Row 3's exact value 1 + 2**-8 + 2**-30 rounds to 1 + 2**-8 in fp32 in any summation order, then to
+    # 1.0 in bf16; rounding the float64 product to bf16 directly would give 1 + 2**-7.
+    x = np.array([[1.0, 2**-8, 0.0], [1.0, 3 * 2**-8, 0.0], [-1.0, -(2**-8), 0.0], [1.0, 2**-8, 2**-30]],
+                 dtype=np.float32)
+    w = np.array([[1.0, 1.0, 1.0], [2.0, 0.0, 0.0]], dtype=np.float32)
+    got = moe.router_logits(x, w)
+    want = np.array([[1.0, 2.0], [1.0 + 2**-6, 2.0], [-1.0, -2.0], [1.0, 2.0]], dtype=np.float32)
+    assert got.dtype == np.float32 and np.array_equal(got, want)
+    # orientation: logits[t, e] = sum_d x[t, d] * router_weight[e, d] (hand-computed, all exact)
+    x = np.array([[1, 2, 3, 4], [0.5, 0, -1, 2]], dtype=np.float32)
+    w = np.array([[1, 0, 0, 0], [0, 1, 1, 0], [0.25, 0.25, 0.25, 0.25]], dtype=np.float32)
+    assert np.array_equal(moe.router_logits(x, w), np.array([[1, 5, 2.5], [0.5, -1, 0.375]], np.float32))
+
+
+def test_composed_moe_on_forced_routing_equals_the_experts():
+    # A router whose logits are known exactly (only column 0 of the router weight is non-zero and every
+    # token has x[:, 0] = 1, so logits[t, e] = c[e]) and a bias of +1 on four chosen experts, two in each
+    # of groups 0 and 1: those two groups are kept and the four are the picks, whatever the other scores.
+    # The weights are then sigmoid(c) of the picks (unbiased), renormalized, times 2.5 -- computed here
+    # in float64 -- and the shared expert adds at weight 1. A biased weight, a dropped scale factor or a
+    # wrong shared-slot weight fails (the group axis is pinned by the per-token loop below).
+    rng = _rng(7)
+    n_routed, g, tg, topk, d, inter, t = 16, 4, 2, 4, 128, 128, 5
+    w1, s1, w2, s2 = _weights(rng, n_routed + 1, inter, d)
+    c = formats.round_to_bf16(rng.uniform(-2, 2, size=n_routed).astype(np.float32))
+    wr = np.zeros((n_routed, d), np.float32)
+    wr[:, 0] = c
+    x = formats.round_to_bf16(rng.normal(size=(t, d)).astype(np.float32))
+    x[:, 0] = 1.0
+    chosen = [1, 2, 5, 6]
+    bias = np.zeros(n_routed, np.float32)
+    bias[chosen] = 1.0
+    got = moe.deepseek_v2_fp8_moe(x, wr, bias, w1, s1, w2, s2, topk, g, tg, True, 2.5)
+    sig = 1.0 / (1.0 + np.exp(-c.astype(np.float64)))
+    order = sorted(chosen, key=lambda e: (-sig[e], e))
+    wts = sig[order] / sig[order].sum() * 2.5
+    ids = np.tile(np.array(order + [n_routed], np.int32), (t, 1))
+    weights = np.tile(np.append(wts, 1.0).astype(np.float32), (t, 1))
+    want = moe.moe_experts(x, ids, weights, w1, s1, w2, s2)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+    # and the picks themselves
+    r_ids, r_w = moe.grouped_topk(moe.router_logits(x, wr), bias, topk, g, tg, True, 2.5)
+    assert np.array_equal(r_ids, ids[:, :topk])
+    np.testing.assert_allclose(r_w, weights[:, :topk], rtol=1e-6)
+
+
+def _brute_route(logit_row, bias, topk, n_groups, topk_group, factor):
+    """One token's grouped top-k by explicit loops in float64 (deepseek_v2/reference.py:121-143): the
+    group score as the two best biased scores summed, groups then experts taken by repeated maximum,
+    the lower index first among equals."""
+    import math
+
+    scores = [1.0 / (1.0 + math.exp(-float(v))) for v in logit_row]
+    biased = [s + float(b) for s, b in zip(scores, bias)]
+    per = len(biased) // n_groups
+    gscore = []
+    for gi in range(n_groups):
+        vals = sorted(biased[gi * per:(gi + 1) * per], reverse=True)
+        gscore.append(vals[0] + vals[1])
+    kept = []
+    for _ in range(topk_group):
+        kept.append(max((v, -i) for i, v in enumerate(gscore) if i not in kept)[1] * -1)
+    ids = []
+    for _ in range(topk):
+        ids.append(max((biased[i], -i) for i in range(len(biased)) if i // per in kept and i not in ids)[1] * -1)
+    w = [scores[i] for i in ids]
+    return ids, [v / sum(w) * factor for v in w]
+
+
+def test_composed_moe_against_a_per_token_loop():
+    # the whole oracle op against an independent per-token construction: logits by exact sums (fsum)
+    # rounded to fp32 then bf16, the routing by _brute_route, each token's slots through the pinned
+    # expert MLP one token at a time, the shared expert last at weight 1
+    import math
+
+    rng = _rng(8)
+    n_routed, g, tg, topk, d, inter, t = 16, 4, 2, 4, 128, 128, 6
+    w1, s1, w2, s2 = _weights(rng, n_routed + 1, inter, d)
+    x = formats.round_to_bf16(rng.normal(size=(t, d)).astype(np.float32))
+    wr = formats.round_to_bf16(rng.normal(scale=0.2, size=(n_routed, d)).astype(np.float32))
+    bias = formats.round_to_bf16(rng.normal(scale=0.05, size=n_routed).astype(np.float32))
+    got = moe.deepseek_v2_fp8_moe(x, wr, bias, w1, s1, w2, s2, topk, g, tg, True, 2.5)
+    for i in range(t):
+        logit = [formats.round_to_bf16(np.array([math.fsum(float(a) * float(b) for a, b in zip(x[i], wr[e]))],
+                                                np.float32))[0] for e in range(n_routed)]
+        ids, wts = _brute_route(logit, bias, topk, g, tg, 2.5)
+        want = moe.expert_mlp(x[i:i + 1], w1[n_routed], s1[n_routed], w2[n_routed], s2[n_routed])[0].astype(np.float64)
+        for e, wt in zip(ids, wts):
+            want += wt * moe.expert_mlp(x[i:i + 1], w1[e], s1[e], w2[e], s2[e])[0]
+        np.testing.assert_allclose(got[i], want, rtol=2e-4, atol=2e-4 * np.abs(want).max())
