@@ -62,6 +62,7 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_size, _vp],
     ),
+    "aklr_probe_hbm_read": (_c_int, [_vp, _c_i64, _vp, _c_int, _c_int, _vp]),
 }
 
 # enums of include/aklr_amd.h

@@ -367,20 +367,11 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
 #pragma unroll
     for (int j = 0; j < D - 1; ++j)
       if (full + j < len) step(kb_begin + full + j, f[j], xr[QA ? j : 0]);
-    if (p.splits > 1) {
-      // partials in accumulator order, [split][group][wave][tile][lane] x 4 fp32: the workgroup that
-      // reduces them runs the same lanes over the same tiles, so every store and load is 1 KiB of
-      // contiguous full lines
-      const rsrc_t prs = partial_rsrc(p.partial, split, stream_plane);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) store_partial4(prs, part_base + (mt * NT + nt) * 256, acc[mt][nt]);
-    }
   }
 
   if constexpr (KW > 1) {
-    // The K groups' sums meet in LDS and group 0 adds them in group order (the plan runs one K split).
+    // The K groups' sums meet in LDS and the waves of group 0 add them in group order. Every wave stays
+    // until past the split-K arrival's barriers, then only group 0's waves go on.
     if (w < NW && kw > 0) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
@@ -388,18 +379,30 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
         for (int nt = 0; nt < NT; ++nt) sRed[(((w - kWC) * MT + mt) * NT + nt) * 64 + lane] = acc[mt][nt];
     }
     __syncthreads();
-    if (w == NW || kw > 0) return;
+    if (w < kWC) {
 #pragma unroll
-    for (int j = 1; j < KW; ++j)
+      for (int j = 1; j < KW; ++j)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] += sRed[((((j - 1) * kWC + w) * MT + mt) * NT + nt) * 64 + lane];
+          for (int nt = 0; nt < NT; ++nt)
+            acc[mt][nt] += sRed[((((j - 1) * kWC + w) * MT + mt) * NT + nt) * 64 + lane];
+    }
   }
 
   if (p.splits > 1) {
+    if (w < kWC) {
+      // partials in accumulator order, [split][group][wave][tile][lane] x 4 fp32 (the waves of K group 0,
+      // which hold the workgroup's sums): the workgroup that reduces them runs the same lanes over the
+      // same tiles, so every store and load is 1 KiB of contiguous full lines
+      const rsrc_t prs = partial_rsrc(p.partial, split, stream_plane);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) store_partial4(prs, part_base + (mt * NT + nt) * 256, acc[mt][nt]);
+    }
     if (!splitk_arrive(p.counters + blockIdx.x, seen, p.splits, &arrive_slot, kArriver)) return;
-    if (w == NW) return;
+    if (w >= kWC) return;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -432,7 +435,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
       }
     }
   }
-  if (w == NW) return;
+  if (w >= kWC) return;  // the loader, and the K groups past the first
 
   // Output. Even NT: for each pair of column tiles a lane packs its 4 columns of each into two words
   // and permlane16_swap exchanges the odd lane groups of the first with the even lane groups of the

@@ -5,8 +5,10 @@ decode FP8 block-scaled GEMM, M in {1, 4, 16, 64, 128} x (N, K) in {(2112, 7168)
 (7168, 16384)}. One step = for each of the 15 (M, N, K): per_group_quant_fp8 of the bf16 activations
 (N(0,1), 1% x20 outliers) then the 128x128-block-scaled GEMM against e4m3 weights (N(0,0.02), 128x128
 fp32 block scales) in aiter's preshuffled layout with the quantizer's column-major scales, bf16 out.
-Each step is one HIP graph; steps rotate over enough weight copies (> 512 MB per shape) that the
-256 MB MALL holds none of them, so weights stream from HBM as in serving.
+Each step is one HIP graph. Every GEMM of a step reads its own weight copy: a shape's five GEMMs (one
+per M) take five consecutive copies of a rotation of > 512 MB per shape, so no copy is read again
+before more than a step's worth of other bytes (888 MB) has passed through the 256 MB MALL -- weights
+stream from HBM, as in serving.
 
 value = whole-step algorithmic bytes / step time, in GB/s (bytes per GEMM: M*K + 4*M*K/128 + N*K +
 4*ceil(N/128)*K/128 + 2*M*N; per quant: 3.03125*M*K).
@@ -24,15 +26,21 @@ runs on cold operands too (rotating > 512 MB of copies), and the figure is the m
 >= 50 ms of warm-up replays. Below ~10 us the reference's figure includes its
 timer's ~4.2 us floor, so only the larger shapes compare kernels.
 prefill / mxfp4: extra figures (TFLOP/s vs the dense FP8 5.0 PF / MXFP4 10.1 PF peaks): FP8 at
-M in {1024, 4096, 8192} (median of 10 launches after >= 50 ms of warm-up launches), MXFP4 at M in
-{1, 32, 512, 4096} (M <= 32 as GB/s vs 8 TB/s).
+M in {1024, 4096, 8192}, MXFP4 at M in {1, 32, 512, 4096} (M <= 32 as GB/s vs 8 TB/s). Every call reads
+cold operands: a graph runs the GEMM over rotating copies of its operands (activations and weights,
+> 512 MB in all), and a figure is the median over 10 replays, after >= 50 ms of warm-up replays, of the
+replay time over the copies.
+decode_floor: the same timing of a kernel that only reads each decode shape's M=1 bytes (the calibration
+kernel aklr_probe_hbm_read, best launch shape) and of an empty kernel: the floor a decode GEMM of that
+size cannot beat here.
 quant: the three activation quantizers at H=7168, T in {2048, 16384} (rows a1/a4/a5), next to the
 reference's recorded times where it has them.
 moe: the grouped DeepSeek-V3 FP8 MoE experts (256 routed + 1 shared, top-8,
 D=7168, I=2048, e4m3 weights with 128x128 scales) on Zipf(1.1) routing at T in {64, 4096}: time per
 call, touched-weight bytes / time vs 8 TB/s, and TFLOP/s vs 5.0 PF.
-cpu_baseline: the CPU oracle (numpy dequantize + fp32 matmul, the reference check's formula) on a
-bounded sample (decode M=16, the three shapes), timed on the host in the same run.
+cpu_baseline: the CPU oracle (numpy quantize, dequantize, fp32 matmul: the reference check's formula)
+on one whole decode step (the same 15 quantize-then-GEMM pairs), timed on the host in the same run:
+the median of 3 repetitions after a warm-up one.
 """
 from __future__ import annotations
 
@@ -129,13 +137,16 @@ def build_decode(dev, shuffled=True):
             copies.append((layouts.shuffle_weight(b) if shuffled else b, bs))
         weights[(n, k)] = copies
     xs = {(m, k): workloads.activations(m, k, seed=m * 7 + k, device=dev) for m in ms for (_, k) in shapes}
-    n_sets = max(len(c) for c in weights.values())
+    # step r's GEMM i of a shape reads copy (r * len(ms) + i) of that shape's rotation; enough steps to
+    # go round the longest rotation
+    n_sets = max(-(-len(c) // len(ms)) for c in weights.values())
 
     def step_fn(r):
         def run():
             for (n, k) in shapes:
-                b, bs = weights[(n, k)][r % len(weights[(n, k)])]
-                for m in ms:
+                rot = weights[(n, k)]
+                for i, m in enumerate(ms):
+                    b, bs = rot[(r * len(ms) + i) % len(rot)]
                     q, s = aklr_amd.per_group_quant_fp8(xs[(m, k)])
                     if shuffled:
                         aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s.view(m, k // 128), bs,
@@ -156,11 +167,14 @@ def fused_step_fn(weights, xs, shuffled):
 
     fmt = "none:preshuffled" if shuffled else "none:none"
 
+    ms = workloads.DECODE_M
+
     def step_fn(r):
         def run():
             for (n, k) in workloads.DEEPSEEK_NK:
-                b, bs = weights[(n, k)][r % len(weights[(n, k)])]
-                for m in workloads.DECODE_M:
+                rot = weights[(n, k)]
+                for i, m in enumerate(ms):
+                    b, bs = rot[(r * len(ms) + i) % len(rot)]
                     aklr_amd.quant_gemm_a8w8_blockwise_scaled(xs[(m, k)], b, bs, operand_format=fmt)
         return run
     return step_fn
@@ -191,18 +205,29 @@ def time_gemm8(dev, m, n, k, weights, steps, stream, shuffled=True, calls_per_gr
 
 
 def prefill_figures(dev, stream, steps=10):
+    """FP8 prefill: each call on cold operands, rotating > 512 MB of (activation, weight)
+    copies inside one graph; the median replay time over the copies."""
     import aklr_amd
     from aklr_amd import layouts, workloads
 
     out = []
     for m, (n, k) in ((m, nk) for m in workloads.PREFILL_M for nk in workloads.DEEPSEEK_NK):
-        x = workloads.activations(m, k, seed=1, device=dev)
-        q, s = aklr_amd.per_group_quant_fp8(x)
-        b, bs = workloads.blockwise_fp8_weight(n, k, seed=2, device=dev)
-        bsh = layouts.shuffle_weight(b)
-        g = _capture(lambda: aklr_amd.gemm_a8w8_blockwise_scaled(q, bsh, s.view(m, k // 128), bs,
-                                                                 operand_format="none:preshuffled"), stream)
-        t = _replay_median_ms(g, steps, 2, stream)
+        copies = []
+        for r in range(_copies(gemm8_bytes(m, n, k), lo=2)):
+            x = workloads.activations(m, k, seed=1 + r, device=dev)
+            q, s = aklr_amd.per_group_quant_fp8(x)
+            b, bs = workloads.blockwise_fp8_weight(n, k, seed=2 + r, device=dev)
+            copies.append((q, s.view(m, k // 128), layouts.shuffle_weight(b), bs))
+            del x, b
+
+        def run(copies=copies):
+            for q, s, b, bs in copies:
+                aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s, bs, operand_format="none:preshuffled")
+
+        g = _capture(run, stream)
+        t = _replay_median_ms(g, steps, 2, stream) / len(copies)
+        del g, copies
+        torch.cuda.empty_cache()
         tf = 2.0 * m * n * k / (t * 1e-3) / 1e12
         out.append({"m": m, "n": n, "k": k, "us": round(t * 1e3, 2), "tflops": round(tf, 1),
                     "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)})
@@ -277,20 +302,25 @@ def mxfp4_figures(dev, stream, steps=10):
     out = []
     for m in workloads.MXFP4_M:  # m <= 32 reported against HBM, m >= 512 against the MXFP4 MFMA peak
         for (n, k) in workloads.LLAMA70B_NK:
-            x = workloads.activations(m, k, seed=1, device=dev)
-            qa, sa = aklr_amd.dynamic_mxfp4_quant(x, shuffle=True)
-            per = gemm4_bytes(0, n, k)
+            # every call on cold operands: rotating (activation, weight) copies of > 512 MB in all
             copies = []
-            for r in range(_copies(per, lo=2) if m <= 32 else 1):
+            for r in range(_copies(gemm4_bytes(m, n, k), lo=2)):
+                x = workloads.activations(m, k, seed=1 + r, device=dev)
+                qa, sa = aklr_amd.dynamic_mxfp4_quant(x, shuffle=True)
                 wb, sb = workloads.mxfp4_weight(n, k, seed=10 + r, device=dev)
-                copies.append((layouts.shuffle_weight(wb), layouts.e8m0_scales(sb)))
+                copies.append((qa, sa, layouts.shuffle_weight(wb), layouts.e8m0_scales(sb)))
+                del x, wb
 
-            def run(copies=copies, qa=qa, sa=sa):
-                for wb, sb in copies:
+            def run(copies=copies):
+                for qa, sa, wb, sb in copies:
                     aklr_amd.gemm_a4w4_mxfp4(qa, wb, sa, sb)
 
             g = _capture(run, stream)
-            t = _replay_time_ms([g], steps, 2, stream) / len(copies)
+            if m <= 32:
+                t = _replay_time_ms([g], steps, 2, stream) / len(copies)
+            else:  # compute-bound: after the clocks settle, as the FP8 prefill figures
+                t = _replay_median_ms(g, steps, 2, stream) / len(copies)
+            del g
             rec = {"m": m, "n": n, "k": k, "us": round(t * 1e3, 2)}
             if m <= 32:
                 gbs = gemm4_bytes(m, n, k) / (t * 1e-3) / 1e9
@@ -396,6 +426,59 @@ def moe_figures(dev, steps=10):
     return out
 
 
+def decode_floor_figures(dev, stream, weights=None, steps=20):
+    """What a kernel that only reads a decode GEMM's bytes takes on this GPU, timed exactly as the GEMMs
+    are (back-to-back launches in one graph over rotating buffers of > 512 MB, HIP events on the launch
+    stream): the calibration kernel aklr_probe_hbm_read (16-byte non-temporal loads, the best of 256,
+    512 and 1024 workgroups with 4 or 8 loads a lane in flight) on the M=1 algorithmic bytes of each
+    DeepSeek-V3 decode shape, an empty kernel (the launch floor), and the GEMM at M=1 and M=16 next
+    to them."""
+    from aklr_amd import _lib, workloads
+
+    lib = _lib.lib()
+    st = stream.cuda_stream
+    sink = torch.empty(1024 * 256, dtype=torch.int32, device=dev)
+    empty = torch.empty(16, dtype=torch.uint8, device=dev)
+
+    def launches(fn, count):
+        g = _capture(lambda: [fn() for _ in range(count)], stream)
+        t = _replay_time_ms([g], steps, 2, stream) / count
+        del g
+        return t
+
+    out = {"empty_kernel_us": round(launches(lambda: lib.aklr_probe_hbm_read(empty.data_ptr(), 0, sink.data_ptr(),
+                                                                             256, 4, st), 32) * 1e3, 2),
+           "shapes": []}
+    for (n, k) in workloads.DEEPSEEK_NK:
+        nbytes = gemm8_bytes(1, n, k)
+        bufs = [torch.empty((nbytes + 15) // 16 * 16, dtype=torch.uint8, device=dev).fill_(1)
+                for _ in range(_copies(nbytes, lo=4))]
+        best = None
+        for wg in (256, 512, 1024):
+            for unroll in (4, 8):
+                def run(wg=wg, unroll=unroll):
+                    for b in bufs:
+                        lib.aklr_probe_hbm_read(b.data_ptr(), nbytes, sink.data_ptr(), wg, unroll, st)
+
+                g = _capture(run, stream)
+                t = _replay_time_ms([g], steps, 2, stream) / len(bufs)
+                del g
+                if best is None or t < best[0]:
+                    best = (t, wg, unroll)
+        rec = {"n": n, "k": k, "bytes": nbytes, "read_us": round(best[0] * 1e3, 2),
+               "read_gbs": round(nbytes / (best[0] * 1e-3) / 1e9, 1), "read_workgroups": best[1],
+               "read_unroll": best[2]}
+        del bufs
+        if weights is not None:
+            for m in (1, 16):
+                t = time_gemm8(dev, m, n, k, weights, steps, stream)
+                rec[f"gemm_m{m}_us"] = round(t * 1e3, 2)
+                rec[f"gemm_m{m}_vs_read"] = round(best[0] / t, 3)
+        out["shapes"].append(rec)
+        torch.cuda.empty_cache()
+    return out
+
+
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "gemm8_stream_m16_n7168_k16384_traffic.json")
 
@@ -434,30 +517,35 @@ def load_traffic():
 
 
 def cpu_baseline():
-    """The CPU oracle on decode M=16 over the three DeepSeek shapes (quantize + dequantize + fp32
-    matmul), one timed repetition after a warm-up of the smallest shape."""
+    """The CPU oracle on one whole decode step (the 15 quantize-then-GEMM pairs: quantize, dequantize,
+    fp32 matmul), the median of 3 timed repetitions after a warm-up one."""
     import numpy as np
 
     from aklr_amd import workloads
     from oracle import gemm as ogemm
     from oracle import quant as oquant
 
-    m = 16
     cases = []
     for (n, k) in workloads.DEEPSEEK_NK:
-        x = workloads.activations(m, k, seed=3, device="cpu")
         b, bs = workloads.blockwise_fp8_weight(n, k, seed=4, device="cpu")
-        cases.append((x.view(torch.int16).numpy().view(np.uint16), b.view(torch.uint8).numpy(), bs.numpy(), n, k))
-    xb, b, bs, n, k = cases[0]
-    q, s = oquant.per_group_quant_fp8(xb)
-    ogemm.gemm_a8w8_blockwise_scaled(q, b, s, bs, scale_major_mode="MN")
-    total_bytes = 0
-    t0 = time.perf_counter()
-    for xb, b, bs, n, k in cases:
-        q, s = oquant.per_group_quant_fp8(xb)
-        ogemm.gemm_a8w8_blockwise_scaled(q, b, s, bs, scale_major_mode="MN")
-        total_bytes += gemm8_bytes(m, n, k) + quant8_bytes(m, k)
-    dt = time.perf_counter() - t0
+        b, bs = b.view(torch.uint8).numpy(), bs.numpy()
+        for m in workloads.DECODE_M:
+            x = workloads.activations(m, k, seed=3 + m, device="cpu")
+            cases.append((x.view(torch.int16).numpy().view(np.uint16), b, bs, m, n, k))
+    total_bytes = sum(gemm8_bytes(m, n, k) + quant8_bytes(m, k) for _, _, _, m, n, k in cases)
+
+    def step():
+        for xb, b, bs, m, n, k in cases:
+            q, s = oquant.per_group_quant_fp8(xb)
+            ogemm.gemm_a8w8_blockwise_scaled(q, b, s, bs, scale_major_mode="MN")
+
+    step()
+    reps = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        step()
+        reps.append(time.perf_counter() - t0)
+    dt = sorted(reps)[1]
     try:
         from threadpoolctl import threadpool_info
 
@@ -469,8 +557,8 @@ def cpu_baseline():
         "unit": "GB/s",
         "cores": int(cores),
         "kind": "port",
-        "sample": f"decode M=16 x (N,K) in (2112,7168),(24576,1536),(7168,16384): quant + dequant + fp32 "
-                  f"matmul, 1 rep, {dt:.2f} s",
+        "sample": f"one decode step, M in {{1,4,16,64,128}} x (N,K) in (2112,7168),(24576,1536),(7168,16384): "
+                  f"quant + dequant + fp32 matmul, median of 3 reps ({', '.join(f'{r:.2f}' for r in reps)} s)",
     }
 
 
@@ -484,6 +572,9 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--probe-traffic", action="store_true",
                     help="only run the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--probe-floor", action="store_true",
+                    help="only time the decode floors: an empty kernel and a pure HBM read of each decode "
+                         "shape's bytes, beside the GEMM (for rocprofv3 --kernel-trace)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -497,6 +588,10 @@ def main(argv=None):
     torch.cuda.set_stream(stream)
     if args.probe_traffic:
         probe_traffic(dev, stream)
+        return 0
+    if args.probe_floor:
+        step_fn, n_sets, step_bytes, weights, xs = build_decode(dev, True)
+        print(json.dumps(decode_floor_figures(dev, stream, weights)), flush=True)
         return 0
     shuffled = args.layout == "preshuffled"
     print(f"[bench] building decode workload ({args.layout})", file=sys.stderr, flush=True)
@@ -522,11 +617,13 @@ def main(argv=None):
             t = time_gemm8(dev, m, n, k, weights, 10, stream, shuffled)
             per_shape.append({"m": m, "n": n, "k": k, "us": round(t * 1e3, 2),
                               "gbs": round(gemm8_bytes(m, n, k) / (t * 1e-3) / 1e9, 1)})
+    floor = decode_floor_figures(dev, stream)
     del graphs, weights
     torch.cuda.empty_cache()
 
     extras = {"decode_fused_quant": {"ms_per_step": round(ms_fused, 4),
-                                     "speedup_vs_two_ops": round(ms_per_step / ms_fused, 3)}}
+                                     "speedup_vs_two_ops": round(ms_per_step / ms_fused, 3)},
+              "decode_floor": floor}
     if not args.no_extras:
         print("[bench] prefill and MXFP4 figures", file=sys.stderr, flush=True)
         extras["prefill_fp8"] = prefill_figures(dev, stream)

@@ -228,6 +228,17 @@ int aklr_moe_fp8_experts(const void* hidden, int64_t tokens, int64_t model_dim, 
                          const void* w2, const float* w2_scale, int w_layout, void* out, void* workspace,
                          size_t workspace_bytes, hipStream_t stream);
 
+/*
+ * Calibration kernel for the decode roofline (no counterpart in the reference): reads `bytes` from
+ * `src` with the decode GEMM's access pattern -- 16-byte non-temporal loads, `unroll` (4 or 8) per lane
+ * in flight, `workgroups` workgroups of 256 lanes each streaming one contiguous chunk -- and nothing
+ * else, so back-to-back launches time the floor of a kernel that reads that many bytes (launch,
+ * first-load latency, stream). bytes = 0 is an empty kernel (the launch floor). sink: uint32
+ * [workgroups * 256], written only if the data fold to one particular word.
+ */
+int aklr_probe_hbm_read(const void* src, int64_t bytes, uint32_t* sink, int workgroups, int unroll,
+                        hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
