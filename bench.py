@@ -479,6 +479,31 @@ def decode_floor_figures(dev, stream, weights=None, steps=20):
     return out
 
 
+def probe_prefill(dev, stream, calls=6):
+    """The program the prefill counters are read on: the FP8 prefill GEMM at M=4096 on the three
+    DeepSeek-V3 shapes (the 256x192, 256x224 and 256x256 LDS plans), each called ``calls`` times on
+    rotating cold operand copies, after one warm-up call per copy."""
+    import aklr_amd
+    from aklr_amd import layouts, workloads
+
+    m = 4096
+    for (n, k) in workloads.DEEPSEEK_NK:
+        copies = []
+        for r in range(_copies(gemm8_bytes(m, n, k), lo=2)):
+            x = workloads.activations(m, k, seed=1 + r, device=dev)
+            q, s = aklr_amd.per_group_quant_fp8(x)
+            b, bs = workloads.blockwise_fp8_weight(n, k, seed=2 + r, device=dev)
+            copies.append((q, s.view(m, k // 128), layouts.shuffle_weight(b), bs))
+            del x, b
+        for i in range(len(copies) + calls):
+            q, s, b, bs = copies[i % len(copies)]
+            aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s, bs, operand_format="none:preshuffled")
+        torch.cuda.synchronize()
+        print(f"[bench] prefill probe m={m} n={n} k={k}: {len(copies) + calls} calls", file=sys.stderr, flush=True)
+        del copies
+        torch.cuda.empty_cache()
+
+
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "gemm8_stream_m16_n7168_k16384_traffic.json")
 
@@ -572,6 +597,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--probe-traffic", action="store_true",
                     help="only run the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--probe-prefill", action="store_true",
+                    help="only run the FP8 prefill GEMM at M=4096 on the three shapes (for rocprofv3 --pmc)")
     ap.add_argument("--probe-floor", action="store_true",
                     help="only time the decode floors: an empty kernel and a pure HBM read of each decode "
                          "shape's bytes, beside the GEMM (for rocprofv3 --kernel-trace)")
@@ -588,6 +615,9 @@ def main(argv=None):
     torch.cuda.set_stream(stream)
     if args.probe_traffic:
         probe_traffic(dev, stream)
+        return 0
+    if args.probe_prefill:
+        probe_prefill(dev, stream)
         return 0
     if args.probe_floor:
         step_fn, n_sets, step_bytes, weights, xs = build_decode(dev, True)
