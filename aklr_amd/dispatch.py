@@ -58,6 +58,7 @@ class KernelInfo:
 ENV_DISABLE = "AKLR_DISABLE"
 ENV_TRACE = "AKLR_TRACE"
 ENV_AITER_PLUGIN = "AKLR_AITER_PLUGIN"
+ENV_SGLANG_PLUGIN = "AKLR_SGLANG_PLUGIN"
 
 
 def all_disabled() -> bool:
@@ -87,8 +88,33 @@ def aiter_plugin_enabled() -> bool:
     return value == "1"
 
 
+def sglang_plugin_enabled() -> bool:
+    """``AKLR_SGLANG_PLUGIN``: "1" hooks sglang's layers to this library's ops, "0" or unset does not;
+    any other value raises (aklr/core/platform/env.py:68-72)."""
+    value = os.environ.get(ENV_SGLANG_PLUGIN) or "0"
+    if value not in ("0", "1"):
+        raise ValueError(f"{ENV_SGLANG_PLUGIN}={value!r}: expected '1' or '0'")
+    return value == "1"
+
+
 _trace_seen: set = set()
 _trace_lock = threading.Lock()
+
+
+def plugin_trace(host: str, target: str, route: str, fallback) -> None:
+    """With ``AKLR_TRACE`` at "plugin" or "all": log once per (host, target, route, outcome) whether a
+    hooked host function ran this library's route or went back to the host's own code."""
+    if trace_mode() not in ("plugin", "all"):
+        return
+    key = ("plugin", host, target, route, str(fallback))
+    with _trace_lock:
+        if key in _trace_seen:
+            return
+        _trace_seen.add(key)
+    if fallback is None:
+        _LOGGER.info("aklr_amd: %s %s served by %s", host, target, route)
+    else:
+        _LOGGER.info("aklr_amd: %s %s back to %s: %s", host, target, host, fallback.value)
 
 
 def trace(contract_id: str, variant: str | None, outcome) -> None:

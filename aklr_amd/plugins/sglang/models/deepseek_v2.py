@@ -1,0 +1,104 @@
+"""sglang's DeepseekV2MoE.forward_normal through ``deepseek_v2_fp8_moe``
+(aklr/plugins/sglang/models/deepseek_v2/api.py:53-151).
+
+The route hands the layer's router, grouped top-k and experts (the shared expert fused as the last of
+w13/w2's slots) to the op as one call, then does what forward_normal does after its experts: the
+all-reduce over tensor-parallel ranks when the layer reduces its results. Everything the op cannot
+take stays on sglang (returns a FallbackReason, and sglang runs its own forward_normal): a rank's share
+of the experts, the routed experts without the shared one, vision top-k, outputs a later step sums,
+padded rows that sglang's top-k masks, the runtime's checks (moe_blocks), experts in another format
+than fp8 at 128 x 128 blocks (MXFP4 experts included: this library has no MXFP4 MoE), shared experts
+fused inside single-batch overlap, hash routing, and a vision-language correction bias.
+"""
+from __future__ import annotations
+
+from ....dispatch import FallbackReason
+from ....moe import deepseek_v2_fp8_moe
+from ..hook import sglang_route
+from . import moe_blocks
+
+__all__ = ["EXPERT_FORMATS", "moe_call"]
+
+TARGET = "sglang.srt.models.deepseek_v2.DeepseekV2MoE.forward_normal"
+EXPERT_FORMATS = ("Fp8MoEMethod",)
+
+
+@sglang_route(TARGET, versions=("0.5.23",))
+def _moe_forward_normal(
+    self,
+    hidden_states,
+    gemm_output_zero_allocator=None,
+    input_ids=None,
+    input_ids_global=None,
+    skip_shared_experts=False,
+    use_vision_topk=False,
+    return_moe_output=False,
+    leave_output_sum=False,
+):
+    if forward_normal_falls_back(self, skip_shared_experts, use_vision_topk, return_moe_output or leave_output_sum):
+        return FallbackReason.OUT_OF_CONTRACT
+    op, arguments = moe_call(self, hidden_states)
+    out = op(**arguments)
+    if isinstance(out, FallbackReason) or not self.reduce_results:
+        return out
+    from sglang.srt.layers.moe import post_experts_all_reduce
+
+    return post_experts_all_reduce(out)
+
+
+def forward_normal_falls_back(mlp, skip_shared_experts, use_vision_topk, output_left) -> bool:
+    """Whether this forward_normal call stays on sglang. The cheap checks of the call itself go first:
+    a call that skips the shared expert, routes by vision top-k, or leaves its output to a later step."""
+    if skip_shared_experts or use_vision_topk or output_left:
+        return True
+    if _masks_padded_rows() or moe_blocks.runtime_falls_back():
+        return True
+    if moe_blocks.experts_fall_back(mlp.experts, EXPERT_FORMATS):
+        return True
+    return bool(mlp._fuse_shared_experts_inside_sbo or mlp.is_hash or mlp.gate.e_score_correction_bias_vl is not None)
+
+
+def _masks_padded_rows() -> bool:
+    """Whether sglang's top-k masks padded rows in this forward: the bound its forward context holds
+    (sglang 0.5.23 reads it there, no longer as an argument of forward_normal)."""
+    from sglang.srt.model_executor.forward_context import get_forward_context, has_forward_context
+
+    if not has_forward_context():
+        return False
+    bound = get_forward_context().moe_num_token_non_padded
+    return bound is not None and bound() is not None
+
+
+def moe_call(mlp, hidden_states):
+    """The op and its keyword arguments, taken from the module: the router's weight, the top-k config
+    (the routed top-k without the fused shared slot, ungrouped as one group), the experts' weights and
+    their per-block inverse scales."""
+    experts, routing = mlp.experts, mlp.topk.topk_config
+    grouped = routing.use_grouped_topk
+    return deepseek_v2_fp8_moe, {
+        "hidden_states": hidden_states,
+        "router_weight": mlp.gate.weight,
+        "correction_bias": topk_bias(routing, hidden_states.dtype),
+        "w1": experts.w13_weight,
+        "w1_scale": experts.w13_weight_scale_inv,
+        "w2": experts.w2_weight,
+        "w2_scale": experts.w2_weight_scale_inv,
+        "topk": routing.top_k - routing.num_fused_shared_experts,
+        "num_expert_group": routing.num_expert_group if grouped else 1,
+        "topk_group": routing.topk_group if grouped else 1,
+        "renormalize": routing.renormalize,
+        "scoring_func": routing.scoring_func,
+        "routed_scaling_factor": mlp.routed_scaling_factor,
+    }
+
+
+def topk_bias(routing, logits_dtype):
+    """The correction bias as sglang's select_experts gives it to its top-k: aiter's grouped top-k takes
+    the copy in the router logits' dtype that the top-k config keeps (unless sglang's JIT grouped top-k
+    kernel is on); every other top-k takes the bias as held."""
+    from sglang.srt.environ import envs
+    from sglang.srt.layers.moe.topk import _use_aiter
+
+    if _use_aiter and routing.use_grouped_topk and not envs.SGLANG_OPT_USE_JIT_KERNEL_GROUPED_TOPK.get():
+        return routing.correction_bias_for_dtype(logits_dtype)
+    return routing.correction_bias

@@ -178,9 +178,18 @@ def test_enable_and_plugin_entry_points(aiter, monkeypatch):
     assert aiter.state["enabled"] == ["aklr", "other"] and aiter.state["source"] == "test"
     from aklr_amd.plugins import sglang, vllm
 
+    # sglang calls register() with its HookRegistry importable; a stand-in records the start-up hook
+    hooks = []
+    registry = types.ModuleType("sglang.srt.plugins.hook_registry")
+    registry.HookRegistry = types.SimpleNamespace(register=lambda *a: hooks.append(a))
+    registry.HookType = types.SimpleNamespace(AROUND="around", AFTER="after")
+    for name in ("sglang", "sglang.srt", "sglang.srt.plugins"):
+        monkeypatch.setitem(sys.modules, name, types.ModuleType(name))
+    monkeypatch.setitem(sys.modules, "sglang.srt.plugins.hook_registry", registry)
     aiter.state["enabled"] = ["other"]
     monkeypatch.setenv("AKLR_AITER_PLUGIN", "1")
     sglang.register()
+    assert [h[0] for h in hooks] == [sglang.STARTED_AFTER]
     assert aiter.state["enabled"][0] == "aklr"
     aiter.state["enabled"] = ["other"]
     monkeypatch.setenv("AKLR_DISABLE", "1")
