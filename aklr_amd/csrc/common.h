@@ -3,7 +3,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
-#include <stdint.h>
+
+#include <cstdint>
 
 #include "../../include/aklr_amd.h"
 

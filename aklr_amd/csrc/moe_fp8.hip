@@ -682,16 +682,13 @@ static Workspace layout(int64_t T, int64_t S, int64_t D, int64_t I, int64_t E, i
   return w;
 }
 
+// The persistent grid: one workgroup per CU of the current device (the runtime answers from its
+// device table; nothing is kept between calls).
 static int num_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+  return n;
 }
 
 static bool dims_ok(int64_t T, int64_t D, int64_t I, int64_t E, int64_t S) {

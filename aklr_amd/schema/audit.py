@@ -1,0 +1,202 @@
+"""The checks an unmodified AKLR applies to a HIP kernel's sources before anything builds them,
+restated so that a kernel this package writes is known to pass them before it leaves here.
+
+- Source files (aklr/core/contract/spec/_sources.py:24-70, _kernel.py:86-119): relative paths of
+  identifier segments ending in ``.hip`` or ``.h``, sorted and unique, the entry file a ``.hip`` among
+  them; utf-8 text with no control character but the newline (no tab), no byte order mark, one final
+  newline and no blank line before it, and no encoding declaration other than utf-8 in the first two
+  lines. ``kernel.requires`` names the ``hip`` toolchain (_kernel.py:124-135).
+- SH0-SH5 (aklr/core/validation/stages/_audit/_hip.py:22-129), on the text with comments and string
+  and character literals blanked:
+  SH0 no unterminated comment or literal;
+  SH1 ``TORCH_LIBRARY*``/``PYBIND11_MODULE`` only in ``#define TORCH_LIBRARY_EXPAND(ns, m)
+  TORCH_LIBRARY(ns, m)`` and in one ``TORCH_LIBRARY_EXPAND(TORCH_EXTENSION_NAME, m)`` registration, in
+  the entry file;
+  SH2 includes are other sources (relative to the including file or to the root), ``hip/``,
+  ``ATen/``, ``c10/``, ``torch/library.h`` or a listed standard header;
+  SH3 no synchronization, allocation outside torch, IPC, graph or module API, device or process
+  change, environment, I/O, or CUDA name;
+  SH4 no ``static`` or ``__device__`` variable that is not const, no ``__managed__``/``thread_local``;
+  SH5 the entry file begins with a comment.
+
+``findings(kernel)`` returns every violation as ``(rule, path, line, what)``; empty means the kernel
+passes.
+"""
+from __future__ import annotations
+
+import posixpath
+import re
+from typing import Any, Iterator, Mapping
+
+__all__ = ["blank", "findings"]
+
+_SEGMENT = re.compile(r"[A-Za-z_][A-Za-z0-9_]*")
+_CONTROL = re.compile("[\x00-\x09\x0b-\x1f\x7f\x85\u2028\u2029]")
+_CODING = re.compile(r"^[ \t\f]*#.*?coding[:=][ \t]*([-\w.]+)")
+_IDENT = re.compile(r"[A-Za-z_][A-Za-z0-9_]*")
+
+_ALLOWED_HEADER_PREFIXES = ("hip/", "ATen/", "c10/")
+_ALLOWED_HEADERS = frozenset((
+    "torch/library.h", "algorithm", "array", "bit", "cfloat", "climits", "cmath", "cstddef", "cstdint",
+    "cstring", "functional", "initializer_list", "iterator", "limits", "numeric", "optional", "string",
+    "tuple", "type_traits", "utility", "vector",
+))
+# SH3, by identifier: whole names, and families by prefix
+_FORBIDDEN_NAMES = frozenset((
+    "hipDeviceSynchronize", "hipStreamSynchronize", "hipEventSynchronize", "hipSetDevice", "hipDeviceReset",
+    "hipDeviceEnablePeerAccess", "hipLaunchHostFunc", "hipStreamAddCallback",
+    "getenv", "secure_getenv", "setenv", "putenv", "system", "popen", "fopen", "freopen", "dlopen",
+    "printf", "fprintf", "puts", "cout", "cerr", "clog", "exit", "quick_exit", "abort",
+))
+_FORBIDDEN_PREFIXES = ("hipMalloc", "hipFree", "hipHostMalloc", "hipHostFree", "hipExtMalloc", "hipIpc",
+                       "hipStreamCreate", "hipGraph", "hipModule")
+_SYNC_COPY_PREFIXES = ("hipMemcpy", "hipMemset")  # unless an Async form
+_LIBRARY_MACRO = re.compile(r"\bTORCH_LIBRARY\w*|\bPYBIND11_MODULE\b")
+_EXPAND_DEFINE = re.compile(
+    r"#\s*define\s+TORCH_LIBRARY_EXPAND\s*\(\s*(\w+)\s*,\s*(\w+)\s*\)\s*TORCH_LIBRARY\s*\(\s*\1\s*,\s*\2\s*\)")
+_REGISTRATION = re.compile(r"\bTORCH_LIBRARY_EXPAND\s*\(\s*TORCH_EXTENSION_NAME\s*,\s*\w+\s*\)")
+_INCLUDE_LINE = re.compile(r"^[ \t]*#[ \t]*include\b", re.M)
+_INCLUDE_TARGET = re.compile(r"#\s*include\s*(?:<([^>\n]+)>|\"([^\"\n]+)\")")
+
+
+def blank(text: str) -> tuple[str, bool]:
+    """``text`` with every comment and string or character literal replaced by spaces (newlines
+    kept), and whether one of them is left open at the end."""
+    out = list(text)
+    i, n = 0, len(text)
+    while i < n:
+        c = text[i]
+        if text.startswith("//", i):
+            j = text.find("\n", i)
+            j = n if j < 0 else j
+        elif text.startswith("/*", i):
+            j = text.find("*/", i + 2)
+            if j < 0:
+                return "".join(out), True
+            j += 2
+        elif c in "\"'":
+            j = i + 1
+            while j < n and text[j] != c:
+                if text[j] == "\n":
+                    return "".join(out), True
+                j += 2 if text[j] == "\\" else 1
+            if j >= n:
+                return "".join(out), True
+            j += 1
+        else:
+            i += 1
+            continue
+        for p in range(i, j):
+            if out[p] != "\n":
+                out[p] = " "
+        i = j
+    return "".join(out), False
+
+
+def _line(text: str, offset: int) -> int:
+    return text.count("\n", 0, offset) + 1
+
+
+def _content_findings(path: str, content: str) -> Iterator[tuple[str, int, str]]:
+    if not content:
+        yield "source", 1, "empty file"
+        return
+    if content.startswith("\ufeff"):
+        yield "source", 1, "byte order mark"
+    if m := _CONTROL.search(content):
+        yield "source", _line(content, m.start()), f"control character {m.group()!r}"
+    lines = content.split("\n")
+    if lines[-1]:
+        yield "source", len(lines), "no final newline"
+    elif len(lines) > 1 and not lines[-2]:
+        yield "source", len(lines) - 1, "blank line at the end"
+    for number, text in enumerate(lines[:2], 1):
+        if (m := _CODING.match(text)) and m.group(1).lower().replace("_", "-") not in ("utf-8", "utf8"):
+            yield "source", number, f"encoding declaration {m.group(1)!r}"
+
+
+def _forbidden(name: str) -> bool:
+    if name in _FORBIDDEN_NAMES or name.startswith(_FORBIDDEN_PREFIXES):
+        return True
+    for prefix in _SYNC_COPY_PREFIXES:
+        if name.startswith(prefix) and "Async" not in name[len(prefix):]:
+            return True
+    return name.startswith("cuda") and len(name) > 4 and name[4].isupper()
+
+
+def _state(blanked: str) -> Iterator[tuple[int, str]]:
+    """SH4: each ``static``/``__device__`` that declares a variable without const, constexpr or an
+    operator before the declaration ends, and each ``__managed__``/``thread_local``."""
+    for m in _IDENT.finditer(blanked):
+        word = m.group()
+        if word in ("__managed__", "thread_local"):
+            yield m.start(), word
+            continue
+        if word not in ("static", "__device__"):
+            continue
+        end = m.end()
+        stop = min((p for p in (blanked.find(ch, end) for ch in ";{}()") if p >= 0), default=len(blanked))
+        span = blanked[end:stop]
+        if {"const", "constexpr", "operator"} & set(_IDENT.findall(span)):
+            continue
+        if "=" in span or (stop < len(blanked) and blanked[stop] == ";"):
+            yield m.start(), " ".join((word + span + (blanked[stop] if stop < len(blanked) else "")).split())
+
+
+def _source_findings(path: str, text: str, paths: frozenset, entry_file: str) -> Iterator[tuple[str, int, str]]:
+    blanked, unterminated = blank(text)
+    if unterminated:
+        yield "SH0", _line(blanked, len(blanked.rstrip())), "unterminated comment or literal"
+        return
+    allowed = [m.span() for m in _EXPAND_DEFINE.finditer(blanked)]
+    registrations = list(_REGISTRATION.finditer(blanked)) if path == entry_file else []
+    allowed += [m.span() for m in registrations]
+    for m in _LIBRARY_MACRO.finditer(blanked):
+        if not any(a <= m.start() < b for a, b in allowed):
+            yield "SH1", _line(blanked, m.start()), f"{m.group()} outside the one registration"
+    if path == entry_file and len(registrations) != 1:
+        yield "SH1", 1, f"the entry file registers {len(registrations)} times, not once"
+    lines = text.split("\n")
+    for m in _INCLUDE_LINE.finditer(blanked):
+        number = _line(blanked, m.start())
+        target = _INCLUDE_TARGET.match(lines[number - 1].strip())
+        system, local = target.groups() if target else (None, None)
+        if local is not None and any(posixpath.normpath(p) in paths
+                                     for p in (posixpath.join(posixpath.dirname(path), local), local)):
+            continue
+        if system is not None and (system.startswith(_ALLOWED_HEADER_PREFIXES) or system in _ALLOWED_HEADERS):
+            continue
+        yield "SH2", number, f"{lines[number - 1].strip()!r} is neither a source nor an allowed header"
+    for m in _IDENT.finditer(blanked):
+        if _forbidden(m.group()):
+            yield "SH3", _line(blanked, m.start()), f"uses {m.group()}"
+    for offset, what in _state(blanked):
+        yield "SH4", _line(blanked, offset), f"keeps state across calls: {what}"
+    if path == entry_file and not re.match(r"[ \t]*(//[ \t]*\S|/\*)", text):
+        yield "SH5", 1, "does not begin with a comment describing the kernel"
+
+
+def findings(kernel: Mapping[str, Any]) -> list[tuple[str, str, int, str]]:
+    """Every violation of a HIP kernel section, sorted: ``(rule, path, line, what)``."""
+    found: list[tuple[str, str, int, str]] = []
+    sources = kernel.get("sources", [])
+    paths = [s["path"] for s in sources]
+    entry_file, _, symbol = kernel.get("entry_point", "").partition("::")
+    if kernel.get("language") != "hip":
+        found.append(("kernel", "", 0, f"language {kernel.get('language')!r} is not hip"))
+    if not symbol.isidentifier() or not entry_file.endswith(".hip") or entry_file not in paths:
+        found.append(("kernel", entry_file, 0, f"entry point {kernel.get('entry_point')!r} is not <a .hip source>::<name>"))
+    if paths != sorted(set(paths)):
+        found.append(("kernel", "", 0, "source paths are not unique and ascending"))
+    if sources and "hip" not in kernel.get("requires", {}):
+        found.append(("kernel", "", 0, "requires names no hip version"))
+    path_set = frozenset(paths)
+    for s in sources:
+        path, content = s["path"], s["content"]
+        segments = path.split("/")
+        if not (all(_SEGMENT.fullmatch(seg) for seg in segments[:-1])
+                and re.fullmatch(r"[A-Za-z_][A-Za-z0-9_]*\.(hip|h)", segments[-1])):
+            found.append(("source", path, 0, "not a path of identifier segments ending in .hip or .h"))
+        found += [(rule, path, line, what) for rule, line, what in _content_findings(path, content)]
+        found += [(rule, path, line, what) for rule, line, what in _source_findings(path, content, path_set, entry_file)]
+    return sorted(found)

@@ -1,0 +1,100 @@
+"""The text and the name of an AKLR schema file.
+
+A schema file is named by a hash of what its author wrote, and its text has one canonical form; an
+unmodified AKLR rejects a file that differs from either (aklr/ops/README.md:21-24, :67-70). Both
+rules are restated here from their definitions:
+
+- ``sorted_key_json``: json with sorted keys, no whitespace, non-ASCII kept, no NaN
+  (aklr/core/contract/semantics/_workloads.py:17-25);
+- ``json_file_text``: insertion order, two-space indent, a list of only numbers on one line, one
+  final newline (aklr/core/contract/expr.py:108-136);
+- ``authored_parts``: the kernel section and each workload's axes and scalars, workloads sorted by
+  their ``sorted_key_json`` (aklr/core/contract/op.py:902-917);
+- ``schema_uuid``: the first 16 hex digits of sha256 of ``sorted_key_json([name, authored_parts])``
+  (aklr/core/contract/locate.py:114-118);
+- ``content_hash``: sha256 of the entry point and the sources, which names the built extension
+  ``aklr_hip_<16 hex digits>`` (aklr/core/contract/spec/_kernel.py:152-161,
+  aklr/core/runtime/builder/builder.py:105-109).
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+from pathlib import PurePosixPath
+from typing import Any, Mapping
+
+__all__ = [
+    "authored_parts",
+    "content_hash",
+    "extension_name",
+    "json_file_text",
+    "relative_path",
+    "schema_uuid",
+    "sorted_key_json",
+]
+
+
+def sorted_key_json(value: Any) -> str:
+    return json.dumps(value, sort_keys=True, separators=(",", ":"), ensure_ascii=False, allow_nan=False)
+
+
+def _is_number(v: Any) -> bool:
+    return isinstance(v, (int, float)) and not isinstance(v, bool)
+
+
+def _text(value: Any, depth: int) -> str:
+    pad = "  " * (depth + 1)
+    if isinstance(value, dict) and value:
+        if not all(isinstance(key, str) for key in value):
+            raise TypeError(f"json keys must be strings: {list(value)!r}")
+        body = [f"{pad}{json.dumps(key, ensure_ascii=False)}: {_text(v, depth + 1)}" for key, v in value.items()]
+        opening, closing = "{", "}"
+    elif isinstance(value, (list, tuple)) and value:
+        if all(_is_number(v) for v in value):
+            return json.dumps(list(value), allow_nan=False)
+        body = [pad + _text(v, depth + 1) for v in value]
+        opening, closing = "[", "]"
+    else:
+        return json.dumps(value, ensure_ascii=False, allow_nan=False)
+    return opening + "\n" + ",\n".join(body) + "\n" + "  " * depth + closing
+
+
+def json_file_text(obj: Any) -> str:
+    """The committed text of a json file."""
+    return _text(obj, 0) + "\n"
+
+
+def authored_parts(schema: Mapping[str, Any]) -> dict[str, Any]:
+    """What the uuid hashes: the kernel section, and each workload's axes and scalars (never its
+    measurements), the workloads in one order whatever the file's."""
+    workloads = []
+    for w in schema.get("workloads", []):
+        axes = w.get("axes")
+        if not isinstance(axes, Mapping) or not all(isinstance(k, str) and type(v) is int for k, v in axes.items()):
+            raise ValueError(f"workload axes {axes!r} are not names to ints")
+        scalars = w.get("scalars", {})
+        if not isinstance(scalars, Mapping):
+            raise ValueError(f"workload scalars {scalars!r} are not a mapping")
+        workloads.append({"axes": dict(axes), "scalars": dict(scalars)})
+    return {"kernel": schema.get("kernel"), "workloads": sorted(workloads, key=sorted_key_json)}
+
+
+def schema_uuid(schema: Mapping[str, Any]) -> str:
+    text = sorted_key_json([schema["name"], authored_parts(schema)])
+    return hashlib.sha256(text.encode()).hexdigest()[:16]
+
+
+def relative_path(schema: Mapping[str, Any]) -> PurePosixPath:
+    """``<op>/impls/<language>/<name>/<uuid>.json`` below the op's parent directory (``aklr/ops`` or a
+    plugin's ``models``), ``<op>`` being the op directory's name."""
+    return PurePosixPath("impls", schema["kernel"]["language"], schema["name"], f"{schema_uuid(schema)}.json")
+
+
+def content_hash(kernel: Mapping[str, Any]) -> str:
+    parts = {"entry_point": kernel["entry_point"], "sources": [[s["path"], s["content"]] for s in kernel["sources"]]}
+    return hashlib.sha256(sorted_key_json(parts).encode()).hexdigest()
+
+
+def extension_name(kernel: Mapping[str, Any]) -> str:
+    """The extension (and op namespace) AKLR's HIP builder gives the kernel."""
+    return f"aklr_hip_{content_hash(kernel)[:16]}"
