@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: MIT
+# Copyright (C) 2026, Advanced Micro Devices, Inc. All rights reserved.
+# The host protocol and rules here follow aklr/plugins/aiter/provider/__init__.py, whose licence notice this is.
+
 """aklr_amd as a kernel plugin of aiter (``aiter.plugin``; aklr/plugins/aiter/provider/__init__.py).
 
 Before each call of an op aiter routes, aiter asks its enabled providers whether they serve it.

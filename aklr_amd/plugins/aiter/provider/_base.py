@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: MIT
+# Copyright (C) 2026, Advanced Micro Devices, Inc. All rights reserved.
+# The host protocol and rules here follow aklr/plugins/aiter/provider/_base.py, whose licence notice this is.
+
 """What every selector of the aiter provider shares (aklr/plugins/aiter/provider/_base.py:1-97).
 
 - ``selector(op)`` registers the function that answers aiter's ``op``: it takes the call as aiter

@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: MIT
+# Copyright (C) 2026, Advanced Micro Devices, Inc. All rights reserved.
+# The host protocol and rules here follow aklr/plugins/aiter/provider/gemm.py, whose licence notice this is.
+
 """aiter's fp8 GEMMs with a fp32 scale per 128 x 128 of the weight and per 1 x 128 of the
 activations, served by ``gemm_a8w8_blockwise_scaled`` (aklr/plugins/aiter/provider/gemm.py:30-96).
 

@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: MIT
+# Copyright (C) 2026, Advanced Micro Devices, Inc. All rights reserved.
+# The host protocol and rules here follow aklr/plugins/aiter/provider/quant.py, whose licence notice this is.
+
 """aiter's group quantization ``per_group_quant(x, scale, quant_dtype, group_size, transpose_scale,
 num_rows, num_rows_factor, scale_type, scale_layout_m32k4)``, served by ``per_group_quant_fp8``
 (groups of 128, fp32 scales, transposed) and ``per_group_quant_mxfp8`` (groups of 32, e8m0 scales,

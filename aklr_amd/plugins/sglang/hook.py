@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: MIT
+# Copyright (C) 2025-2026, Advanced Micro Devices, Inc. All rights reserved.
+# The host protocol and rules here follow aklr/plugins/sglang/hook.py, whose licence notice this is.
+
 """How a sglang function reaches this library's ops: a route declared next to the op it calls.
 
 Same protocol as aklr/plugins/sglang/hook.py:29-103:

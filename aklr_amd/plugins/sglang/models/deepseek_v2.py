@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: MIT
+# Copyright (C) 2025-2026, Advanced Micro Devices, Inc. All rights reserved.
+# The host protocol and rules here follow aklr/plugins/sglang/models/deepseek_v2/api.py, whose licence notice this is.
+
 """sglang's DeepseekV2MoE.forward_normal through ``deepseek_v2_fp8_moe``
 (aklr/plugins/sglang/models/deepseek_v2/api.py:53-151).
 

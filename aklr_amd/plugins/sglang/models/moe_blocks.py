@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: MIT
+# Copyright (C) 2025-2026, Advanced Micro Devices, Inc. All rights reserved.
+# The host protocol and rules here follow aklr/plugins/sglang/models/moe_blocks.py, whose licence notice this is.
+
 """The checks that keep a sglang MoE call on sglang (aklr/plugins/sglang/models/moe_blocks.py:16-126).
 
 They read sglang's own state: the graph mode and parallel configuration of the running model, and how
