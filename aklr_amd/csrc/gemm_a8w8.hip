@@ -86,7 +86,9 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   constexpr int kLoadsA = KW * (2 * MT + kSRows / 64);  // loader loads per stage
   constexpr int kWC = NW / KW;                          // waves across the columns
   constexpr int kCols = kWC * NT * 16;
-  constexpr int kNBlk = kCols >= 128 ? kCols / 128 : 1;  // 128-column b_scale blocks under the workgroup
+  // 128-column b_scale blocks under the workgroup: its columns start at a multiple of kCols, so a width
+  // that neither divides nor is a multiple of 128 (96, 112) can straddle one more block
+  constexpr int kNBlk = kCols % 128 == 0 ? kCols / 128 : (128 % kCols == 0 ? 1 : kCols / 128 + 2);
   static_assert((NS - 2) * kLoadsA <= 63, "the loader's wait count must fit vmcnt");
   __shared__ __attribute__((aligned(1024))) uint8_t sA[NS][KW * MT * 2048];
   __shared__ __attribute__((aligned(16))) float sS[NS][KW * kSRows];
@@ -871,7 +873,7 @@ static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
 // workgroups of columns: the narrower workgroups then need fewer K splits, so less partial traffic,
 // for the same workgroup count), and K split in up to 4 parts until about 256 workgroups run (each
 // split >= 4 K blocks).
-static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k) {
+static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
   Plan8 p;
   p.kind = Kernel8::kStream;
   p.tm = p.tn = 0;
@@ -909,11 +911,44 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k) {
       }
     }
   }
+  // One row tile on fewer than 240 workgroups leaves CUs idle. Then workgroups of 32, 96 or 112 columns
+  // (1, 3 or 7 compute waves) that make 240-264 workgroups with the same K splits take over: two
+  // column tiles per wave first, then the count nearest 256. The same splits keep every output's
+  // arithmetic that of the 4-wave plan (only the K split changes the order of the sums), so results
+  // stay bitwise the same and the fused-quantization kernel, which keeps the 4-wave plan, agrees with
+  // the two ops. Measured against the 4-wave plan at m = 1 / 16, us: 2112 x 7168 7.76 -> 7.13 / 8.03 ->
+  // 7.84 (32 columns), 2048 x 7168 7.72 -> 6.82 / 7.97 -> 6.95, 24576 x 1536 9.45 -> 8.96 / 9.27 -> 9.18
+  // (96 columns). More splits to fill the chip lost where the 4-wave plan splits K over its waves
+  // (7168 x 2048..4096: +11-16%) and on short K (1024 x 4096: +12-14%).
+  if (fill && p.mt == 1 && p.kw == 1 && (int64_t)p.grid_x * p.splits < 240) {
+    struct Cand { int nw, nt; };
+    constexpr Cand kCands[] = {{1, 2}, {3, 2}, {7, 1}};
+    int64_t best_knt = 2, best_d = 0, best_groups = 0;
+    int best_nw = 0, best_nt = 0;
+    for (const Cand& c : kCands) {
+      const int64_t groups = (n + c.nw * c.nt * 16 - 1) / (c.nw * c.nt * 16), wgs = groups * p.splits;
+      if (wgs < 240 || wgs > 264) continue;
+      const int64_t knt = c.nt == 2 ? 0 : 1, d = wgs > 256 ? wgs - 256 : 256 - wgs;
+      if (knt < best_knt || (knt == best_knt && d < best_d)) {
+        best_knt = knt;
+        best_d = d;
+        best_groups = groups;
+        best_nw = c.nw;
+        best_nt = c.nt;
+      }
+    }
+    if (best_nw > 0) {
+      p.nw = best_nw;
+      p.nt = best_nt;
+      p.grid_x = (int)best_groups;
+    }
+  }
   return p;
 }
 
-static Plan8 plan8(int64_t m, int64_t n, int64_t k) {
-  if (m <= kStreamMaxM) return plan8_stream(m, n, k);
+// fill = false keeps the one-row-tile plans at 4 compute waves (the fused-quantization kernel's shape).
+static Plan8 plan8(int64_t m, int64_t n, int64_t k, bool fill = true) {
+  if (m <= kStreamMaxM) return plan8_stream(m, n, k, fill);
   return plan8_lds_best(m, n, k);
 }
 
@@ -925,12 +960,13 @@ static size_t workspace8(const Plan8& p) {
   return kSplitkCounterBytes + (size_t)p.splits * (size_t)p.grid_x * p.tm * p.tn * sizeof(float);
 }
 
-// Stream kernel: 4 compute waves and 4 A stages; ring depth 4 at 1-2 row tiles, else 2 (measured).
-template <int MT, int NT, int FMT, bool PRE, bool QA = false, int KW = 1>
+// Stream kernel: NW compute waves (4 but for the one-row-tile fill plans) and 4 A stages; ring depth 4
+// at 1-2 row tiles, else 2 (measured).
+template <int MT, int NT, int FMT, bool PRE, bool QA = false, int KW = 1, int NW = 4>
 static void launch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   constexpr int D = MT <= 2 ? 4 : 2;
-  hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, 4, D, 4, FMT, PRE, QA, KW>),
-                     dim3((unsigned)d.grid_x, (unsigned)d.splits), dim3(5 * 64), 0, s, a);
+  hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, NW, D, 4, FMT, PRE, QA, KW>),
+                     dim3((unsigned)d.grid_x, (unsigned)d.splits), dim3((NW + 1) * 64), 0, s, a);
 }
 
 template <int FMT, bool PRE>
@@ -938,6 +974,12 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   if (d.kw > 1) {  // one column tile per wave, 1 or 2 row tiles
     if (d.mt == 1) d.kw == 2 ? launch_stream<1, 1, FMT, PRE, false, 2>(a, d, s) : launch_stream<1, 1, FMT, PRE, false, 4>(a, d, s);
     else d.kw == 2 ? launch_stream<2, 1, FMT, PRE, false, 2>(a, d, s) : launch_stream<2, 1, FMT, PRE, false, 4>(a, d, s);
+  } else if (d.mt == 1 && d.nw == 1) {
+    launch_stream<1, 2, FMT, PRE, false, 1, 1>(a, d, s);
+  } else if (d.mt == 1 && d.nw == 3) {
+    launch_stream<1, 2, FMT, PRE, false, 1, 3>(a, d, s);
+  } else if (d.mt == 1 && d.nw == 7) {
+    launch_stream<1, 1, FMT, PRE, false, 1, 7>(a, d, s);
   } else if (d.mt == 1) d.nt == 2 ? launch_stream<1, 2, FMT, PRE>(a, d, s) : launch_stream<1, 1, FMT, PRE>(a, d, s);
   else if (d.mt == 2) d.nt == 2 ? launch_stream<2, 2, FMT, PRE>(a, d, s) : launch_stream<2, 1, FMT, PRE>(a, d, s);
   else if (d.mt == 4) d.nt == 2 ? launch_stream<4, 2, FMT, PRE>(a, d, s) : launch_stream<4, 1, FMT, PRE>(a, d, s);
@@ -948,7 +990,9 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
 // the workspace and runs the GEMM. Measured on the DeepSeek-V3 shapes: one row tile saves 1-1.5 us a
 // call over the two launches; at 2 row tiles (8 values a lane) the two are even, at 4 (32 values a
 // lane) the quantization outgrows the wait for the weights and the fused call is 15-25% slower.
-static bool fused_quant_ok(const Plan8& p) { return p.kind == Kernel8::kStream && p.mt == 1 && p.kw == 1; }
+static bool fused_quant_ok(const Plan8& p) {
+  return p.kind == Kernel8::kStream && p.mt == 1 && p.kw == 1 && p.nw == 4;
+}
 
 template <bool PRE>
 static void dispatch_stream_qa(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
@@ -1086,12 +1130,12 @@ extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void*
 
 extern "C" size_t aklr_quant_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k < 128) return 0;
-  return quant_gemm_workspace(plan8(m, n, k), m, k);
+  return quant_gemm_workspace(plan8(m, n, k, false), m, k);
 }
 
 extern "C" int aklr_quant_gemm_a8w8_blockscale_fused(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k < 128) return 0;
-  return fused_quant_ok(plan8(m, n, k)) ? 1 : 0;
+  return fused_quant_ok(plan8(m, n, k, false)) ? 1 : 0;
 }
 
 extern "C" int aklr_quant_gemm_a8w8_blockscale(const void* x, int64_t ldx, const void* b, int64_t ldb,
@@ -1111,7 +1155,7 @@ extern "C" int aklr_quant_gemm_a8w8_blockscale(const void* x, int64_t ldx, const
   if (b_layout == AKLR_B_ROW_MAJOR && (ldb < k || ldb % 16 != 0 || ldb >= (1 << 23))) return AKLR_ERR_INVALID_ARGUMENT;
   if (ldbs < k / 128) return AKLR_ERR_INVALID_ARGUMENT;
   if (m == 0) return AKLR_OK;
-  const Plan8 plan = plan8(m, n, k);
+  const Plan8 plan = plan8(m, n, k, false);
   const size_t need = quant_gemm_workspace(plan, m, k);
   if (need > 0 && (!workspace || workspace_bytes < need || !aklr_aligned16(workspace))) return AKLR_ERR_WORKSPACE;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
