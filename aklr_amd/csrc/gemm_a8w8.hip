@@ -943,6 +943,31 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
       p.grid_x = (int)best_groups;
     }
   }
+  // The same at 4 and 8 row tiles, where a workgroup's work is long: 240-256 workgroups (a second
+  // workgroup on a CU doubles that CU's time), one column tile per wave, 2, 6 or 7 compute waves, the
+  // count nearest 256 and then the most waves. Measured against the 4-wave plan at m = 64 / 128, us:
+  // 24576 x 1536 12.64 -> 10.96 / 15.94 -> 15.31 (6 waves), 7168 x 16384 30.02 -> 27.02 / 39.13 -> 38.30
+  // (7 waves), 2048 x 7168 11.06 -> 10.45 / 16.14 -> 14.94 (2 waves); 264 workgroups of 2112 x 7168 lost
+  // 20-30%.
+  if (fill && (p.mt == 4 || p.mt == 8) && p.kw == 1 && (int64_t)p.grid_x * p.splits < 240) {
+    constexpr int kWaves[] = {7, 6, 2};
+    int best_nw = 0;
+    int64_t best_d = 0, best_groups = 0;
+    for (const int nw : kWaves) {
+      const int64_t groups = (n + nw * 16 - 1) / (nw * 16), wgs = groups * p.splits;
+      if (wgs < 240 || wgs > 256) continue;
+      if (best_nw == 0 || 256 - wgs < best_d) {
+        best_nw = nw;
+        best_d = 256 - wgs;
+        best_groups = groups;
+      }
+    }
+    if (best_nw > 0) {
+      p.nw = best_nw;
+      p.nt = 1;
+      p.grid_x = (int)best_groups;
+    }
+  }
   return p;
 }
 
@@ -982,8 +1007,17 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
     launch_stream<1, 1, FMT, PRE, false, 1, 7>(a, d, s);
   } else if (d.mt == 1) d.nt == 2 ? launch_stream<1, 2, FMT, PRE>(a, d, s) : launch_stream<1, 1, FMT, PRE>(a, d, s);
   else if (d.mt == 2) d.nt == 2 ? launch_stream<2, 2, FMT, PRE>(a, d, s) : launch_stream<2, 1, FMT, PRE>(a, d, s);
-  else if (d.mt == 4) d.nt == 2 ? launch_stream<4, 2, FMT, PRE>(a, d, s) : launch_stream<4, 1, FMT, PRE>(a, d, s);
-  else d.nt == 2 ? launch_stream<8, 2, FMT, PRE>(a, d, s) : launch_stream<8, 1, FMT, PRE>(a, d, s);
+  else if (d.mt == 4) {
+    if (d.nw == 2) launch_stream<4, 1, FMT, PRE, false, 1, 2>(a, d, s);
+    else if (d.nw == 6) launch_stream<4, 1, FMT, PRE, false, 1, 6>(a, d, s);
+    else if (d.nw == 7) launch_stream<4, 1, FMT, PRE, false, 1, 7>(a, d, s);
+    else d.nt == 2 ? launch_stream<4, 2, FMT, PRE>(a, d, s) : launch_stream<4, 1, FMT, PRE>(a, d, s);
+  } else {
+    if (d.nw == 2) launch_stream<8, 1, FMT, PRE, false, 1, 2>(a, d, s);
+    else if (d.nw == 6) launch_stream<8, 1, FMT, PRE, false, 1, 6>(a, d, s);
+    else if (d.nw == 7) launch_stream<8, 1, FMT, PRE, false, 1, 7>(a, d, s);
+    else d.nt == 2 ? launch_stream<8, 2, FMT, PRE>(a, d, s) : launch_stream<8, 1, FMT, PRE>(a, d, s);
+  }
 }
 
 // The fused-quantization stream kernel serves plans of one row tile (m <= 16); larger m quantizes into
