@@ -195,6 +195,23 @@ def test_stream_shapes(m, n, k, bias):
     _run_and_check(m, n, k, variant="b_shuffled", bias=False, seed=52)
 
 
+# The planner's fill plans, one per compute-wave count it picks, each with a ragged last column group
+# (some of its waves' columns past n) and column groups straddling 128-column b_scale blocks (widths of
+# 32, 96 and 112 columns): 1 row tile at 1, 3 and 7 waves, 4 and 8 row tiles at 2, 6 and 7 waves.
+@pytest.mark.parametrize("m,n,k,bias,fp16", [
+    (16, 1904, 7168, True, False),     # 1 wave x 2 tiles, 4 splits
+    (4, 22960, 1024, False, True),     # 3 waves x 2 tiles
+    (1, 26784, 1536, True, False),     # 7 waves x 1 tile
+    (64, 1904, 4096, False, False),    # 4 row tiles, 2 waves, 4 splits
+    (96, 5680, 16384, True, True),     # 8 row tiles, 6 waves
+    (50, 6624, 16384, False, False),   # 4 row tiles, 7 waves
+])
+def test_fill_plans(m, n, k, bias, fp16):
+    out_dtype = torch.float16 if fp16 else None
+    _run_and_check(m, n, k, bias=bias, out_dtype=out_dtype, seed=61)
+    _run_and_check(m, n, k, variant="b_shuffled", seed=62)
+
+
 # 192- and 224-column LDS tiles (planned where they divide N): ragged row tiles, bias and fp16 output on
 # the odd last column tile's 8-byte stores, b_scale blocks straddled by a wave's columns (tiles start at
 # multiples of 64 or 32 columns), 256- and 128-row tiles, the 4 x 2 wave layout and the uneven B slabs
