@@ -68,6 +68,39 @@ __device__ __forceinline__ void lds_dma4(const i32x4& rsrc, uint32_t lds, uint32
                : "m0");
 }
 
+// The same loads with the K advance in soffset: the per-lane voffset stays fixed across a loop, so
+// issuing a stage costs no vector instructions. A descriptor whose byte count is 0 reads zeros.
+__device__ __forceinline__ void lds_dma16_so(const i32x4& rsrc, uint32_t lds, uint32_t voffset, uint32_t soffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voffset), "s"(rsrc),
+               "s"(soffset)
+               : "m0");
+}
+__device__ __forceinline__ void lds_dma4_so(const i32x4& rsrc, uint32_t lds, uint32_t voffset, uint32_t soffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(lds), "v"(voffset), "s"(rsrc),
+               "s"(soffset)
+               : "m0");
+}
+
+// Compile-time loop: SFor<0, N>::run(f) calls f(IC<0>{}), ..., f(IC<N - 1>{}), so a generic lambda
+// sees its index as a constant (decltype(i)::value).
+template <int V>
+struct IC {
+  static constexpr int value = V;
+};
+template <int I, int N>
+struct SFor {
+  template <typename F>
+  __device__ __forceinline__ static void run(F& f) {
+    f(IC<I>{});
+    SFor<I + 1, N>::run(f);
+  }
+};
+template <int N>
+struct SFor<N, N> {
+  template <typename F>
+  __device__ __forceinline__ static void run(F&) {}
+};
+
 __device__ __forceinline__ void buf_ld_lds16(rsrc_t r, void* lds, uint32_t voffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, (int)voffset, 0, 0, 0);
 }

@@ -514,8 +514,7 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   constexpr int WN = TN == 224 ? 2 : 4, WM = 8 / WN;  // waves along n and m
   constexpr int MT = TM / (16 * WM), NT = TN / (16 * WN);  // 16x16 tiles per wave along m and n
   // TN = 192 (N = 2112 = 11 x 192) and 224 (N = 7168 = 32 x 224): tiles start at multiples of 64 or
-  // 32 columns, so a wave's columns can straddle 128-column b_scale blocks, and its b_scale is taken
-  // per column tile.
+  // 32 columns, so a wave's columns can straddle two 128-column b_scale blocks.
   constexpr bool kBlkPerTile = TN % 128 != 0;
   constexpr int kNBlk = TN == 224 ? 3 : (TN + 127) / 128;  // 128-column b_scale blocks a tile spans
   // B moves in slabs of 8 rows, BI per wave. When the slabs do not divide evenly (TN = 224: 28 slabs),
@@ -528,6 +527,13 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   constexpr int kLoads = AI + BI + 1;        // + one a_scale load
   constexpr int kStageA = TM * 128, kStageB = BI * 8 * 1024;
   constexpr int kScaleWaves = TM / 64;       // waves whose a_scale load carries rows
+  // Each MFMA's fold runs kLag MFMAs after it (the last kLag of a step at the start of the next), so
+  // its FMAs read a result that is already complete and issue while the matrix core works on later
+  // tiles; folding the newest result instead stalls every step on the MFMA latency (measured 8-10%
+  // slower on 256x224 tiles, bitwise the same output).
+  constexpr int kLag = 3;
+  constexpr int kT = MT * NT;
+  static_assert(kT > kLag, "fold lag");
   __shared__ __attribute__((aligned(1024))) uint8_t sA[S * kStageA];
   __shared__ __attribute__((aligned(1024))) uint8_t sB[S * kStageB];
   __shared__ __attribute__((aligned(16))) float sS[S * TM];
@@ -599,16 +605,22 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   constexpr uint32_t kSlabStrideB = kEvenB ? 1024 : 8 * 1024;  // LDS bytes between a wave's B slabs
   const uint32_t lds_s = scale_wave ? lds_addr(&sS[w * 64]) : lds_addr(&sDummy[w * 64]);
   const uint32_t lds_s_step = scale_wave ? TM * 4 : 0;
+  const uint32_t sa_kstep = (uint32_t)(p.sa_sk * 4);
+  // The lane offsets stay fixed; a stage's K offset rides soffset, so an issue is scalar work only.
+  // A stage past the K range loads through a descriptor of no bytes: zeros, no memory traffic, and
+  // the same load count.
   auto issue = [&](int kb, int st) {
     const bool on = kb < kb_end;
+    i32x4 ra = ars, rb = brs, rs = sars;
+    ra[2] = on ? ars[2] : 0;
+    rb[2] = on ? brs[2] : 0;
+    rs[2] = on ? sars[2] : 0;
     const uint32_t ak = (uint32_t)kb * 128u, bk = PRE ? (uint32_t)kb * 2048u : (uint32_t)kb * 128u;
 #pragma unroll
-    for (int j = 0; j < AI; ++j) lds_dma16(ars, lds_a + st * kStageA + j * 1024, on ? a_off[j] + ak : kOobOffset);
+    for (int j = 0; j < AI; ++j) lds_dma16_so(ra, lds_a + st * kStageA + j * 1024, a_off[j], ak);
 #pragma unroll
-    for (int j = 0; j < BI; ++j)
-      lds_dma16(brs, lds_b + st * kStageB + j * kSlabStrideB, on && b_off[j] != kOobOffset ? b_off[j] + bk : kOobOffset);
-    lds_dma4(sars, lds_s + st * lds_s_step,
-             on && sa_off != kOobOffset ? sa_off + (uint32_t)(kb * p.sa_sk * 4) : kOobOffset);
+    for (int j = 0; j < BI; ++j) lds_dma16_so(rb, lds_b + st * kStageB + j * kSlabStrideB, b_off[j], bk);
+    lds_dma4_so(rs, lds_s + st * lds_s_step, sa_off, (uint32_t)kb * sa_kstep);
   };
 
   f32x4 acc[MT][NT];
@@ -627,60 +639,136 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
       sSB[r][kk] = p.sb[(int64_t)min((n0 >> 7) + r, last_row) * p.ldbs + kb_begin + kk];
     }
   }
-  const float* sbw = sSB[((n0 + wn * (TN / WN)) >> 7) - (n0 >> 7)];
-  int sb_blk[NT];  // kBlkPerTile: each column tile's block
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) sb_blk[nt] = ((n0 + wn * (TN / WN) + nt * 16) >> 7) - (n0 >> 7);
+  // A wave's columns (at most 112) lie in at most two 128-column blocks: block blk0 and, from column
+  // tile split_nt on, blk0 + 1. The K loop is instantiated per split_nt, so a step computes 2 * MT
+  // scale products (a_scale x each block's b_scale) instead of one per MFMA.
+  const int wcol = n0 + wn * (TN / WN);
+  const int blk0 = (wcol >> 7) - (n0 >> 7);
+  const int split_nt = min(NT, (128 - (wcol & 127)) >> 4);
+  const float* sb0 = sSB[blk0];
+  const float* sb1 = sSB[min(blk0 + 1, kNBlk - 1)];
 
   // Fragment addresses: every row a lane reads is congruent to li mod 8, so the swizzle term is the
-  // same for all its row tiles and each read is one base plus an immediate (tile * 2048 bytes).
+  // same for all its row tiles and each read is one base plus an immediate (stage and tile offsets).
   const int swz_lo = (g ^ (li & 7)) << 4, swz_hi = ((4 + g) ^ (li & 7)) << 4;
   const int a_row = (wm * (TM / WM) + li) * 128, b_row = (wn * (TN / WN) + li) * 128;
   const int s_row = wm * (TM / WM) + li;
-  auto compute = [&](int kb, int st) {
-    const float sb = sbw[kb - kb_begin];
-    const uint8_t* A = sA + st * kStageA;
-    const uint8_t* B = sB + st * kStageB;
-    const float* SA = sS + st * TM + s_row;
-    i32x8 bf[NT];
+  // A step holds the smaller set of fragments (A's MT or B's NT) in registers for all its MFMAs and
+  // streams the other, one tile ahead; tile t is (mt, nt) with the streamed index outer.
+  constexpr bool kHoldA = MT <= NT;
+  constexpr int kHeld = kHoldA ? MT : NT, kStreamed = kHoldA ? NT : MT;
+  auto tmt = [](int t) { return kHoldA ? t % MT : t / NT; };
+  auto tnt = [](int t) { return kHoldA ? t / MT : t % NT; };
+  f32x4 pend[kLag];  // the previous step's last kLag partials and their scales
+  float pend_s[kLag];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-      bf[nt] = cat(*reinterpret_cast<const u32x4*>(B + b_row + swz_lo + nt * 2048),
+  for (int j = 0; j < kLag; ++j) {
+    pend[j] = f32x4{0.f, 0.f, 0.f, 0.f};  // folds of zero into the zero accumulators
+    pend_s[j] = 0.f;
+  }
+
+  auto kloop = [&](auto split_c) {
+    constexpr int SPLIT = decltype(split_c)::value;  // first column tile in block blk0 + 1 (NT: none)
+    auto compute = [&](int kb, auto st_c) {
+      constexpr int ST = decltype(st_c)::value;
+      const uint8_t* A = sA + ST * kStageA;
+      const uint8_t* B = sB + ST * kStageB;
+      const float* SA = sS + ST * TM + s_row;
+      auto read_a = [&](int mt) {
+        return cat(*reinterpret_cast<const u32x4*>(A + a_row + swz_lo + mt * 2048),
+                   *reinterpret_cast<const u32x4*>(A + a_row + swz_hi + mt * 2048));
+      };
+      auto read_b = [&](int nt) {
+        return cat(*reinterpret_cast<const u32x4*>(B + b_row + swz_lo + nt * 2048),
                    *reinterpret_cast<const u32x4*>(B + b_row + swz_hi + nt * 2048));
+      };
+      i32x8 held[kHeld];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const i32x8 af = cat(*reinterpret_cast<const u32x4*>(A + a_row + swz_lo + mt * 2048),
-                           *reinterpret_cast<const u32x4*>(A + a_row + swz_hi + mt * 2048));
-      const float sa_row = SA[mt * 16];
-      const float s = sa_row * sb;
+      for (int i = 0; i < kHeld; ++i) held[i] = kHoldA ? read_a(i) : read_b(i);
+      const float sb_lo = sb0[kb - kb_begin];
+      const float sb_hi = SPLIT < NT ? sb1[kb - kb_begin] : 0.f;
+      float sc_lo[MT], sc_hi[MT];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        const f32x4 part = mfma16x128<FMT>(bf[nt], af, z);  // lane: row li, columns 4g..4g+3
-        const float sn = kBlkPerTile ? sa_row * sSB[sb_blk[nt]][kb - kb_begin] : s;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(part[r], sn, acc[mt][nt][r]);
+      for (int mt = 0; mt < MT; ++mt) {
+        const float sa_row = SA[mt * 16];
+        sc_lo[mt] = sa_row * sb_lo;
+        sc_hi[mt] = SPLIT < NT ? sa_row * sb_hi : 0.f;
       }
+      i32x8 cur, nxt = kHoldA ? read_b(0) : read_a(0);
+      f32x4 part[kT];
+      float sc[kT];
+#pragma unroll
+      for (int t = 0; t < kT; ++t) {
+        const int mt = tmt(t), nt = tnt(t);
+        const int si = t / kHeld, hi = t % kHeld;
+        if (hi == 0) {
+          cur = nxt;
+          if (si + 1 < kStreamed) nxt = kHoldA ? read_b(si + 1) : read_a(si + 1);
+        }
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        // lane: row li, columns 4g..4g+3 (the weight is the first operand)
+        part[t] = kHoldA ? mfma16x128<FMT>(cur, held[hi], z) : mfma16x128<FMT>(held[hi], cur, z);
+        sc[t] = nt < SPLIT ? sc_lo[mt] : sc_hi[mt];
+        // The empty asm makes the fold of tile t - kLag (or the previous step's pending tile) come
+        // after MFMA t in the schedule; it emits nothing.
+        if (t >= kLag) {
+          const int u = t - kLag;
+          asm volatile("" : "+v"(part[u]) : "v"(part[t]));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[tmt(u)][tnt(u)][r] = fmaf(part[u][r], sc[u], acc[tmt(u)][tnt(u)][r]);
+        } else {
+          const int u = kT - kLag + t;
+          asm volatile("" : "+v"(pend[t]) : "v"(part[t]));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[tmt(u)][tnt(u)][r] = fmaf(pend[t][r], pend_s[t], acc[tmt(u)][tnt(u)][r]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kLag; ++j) {
+        pend[j] = part[kT - kLag + j];
+        pend_s[j] = sc[kT - kLag + j];
+      }
+    };
+    // Stage kb lives in slot (kb - kb_begin) % S. At each step this wave's loads of the stage about to
+    // be computed are waited for (S - 2 younger stages stay in flight), then the barrier makes every
+    // wave's loads visible and guarantees that no wave still reads the slot the next issue refills
+    // (the slot computed one step earlier). The loop runs whole rounds of S steps, so every slot
+    // index is a constant.
+    auto step = [&](int kb, auto st_c) {
+      constexpr int ST = decltype(st_c)::value;
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((S - 2) * kLoads) : "memory");
+      __syncthreads();
+      issue(kb + S - 1, (ST + S - 1) % S);
+      compute(kb, st_c);
+    };
+    int kb = kb_begin;
+    for (; kb + S <= kb_end; kb += S) {
+      auto ring = [&](auto j) { step(kb + decltype(j)::value, j); };
+      SFor<0, S>::run(ring);
     }
+    auto tail = [&](auto j) {
+      if (kb + decltype(j)::value < kb_end) step(kb + decltype(j)::value, j);
+    };
+    SFor<0, S - 1>::run(tail);
   };
 
-  // Stage kb lives in slot (kb - kb_begin) % S. At each step this wave's loads of the stage about to
-  // be computed are waited for (S - 2 younger stages stay in flight), then the barrier makes every
-  // wave's loads visible and guarantees that no wave still reads the slot the next issue refills
-  // (the slot computed one step earlier). Issues past the end of the K range are empty loads, which
-  // keep the wait count exact.
 #pragma unroll
   for (int s = 0; s < S - 1; ++s) issue(kb_begin + s, s);
-  int st = 0, st_fill = S - 1;
-  for (int kb = kb_begin; kb < kb_end; ++kb) {
-    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((S - 2) * kLoads) : "memory");
-    __syncthreads();
-    issue(kb + S - 1, st_fill);
-    compute(kb, st);
-    st = st + 1 == S ? 0 : st + 1;
-    st_fill = st_fill + 1 == S ? 0 : st_fill + 1;
+  if constexpr (!kBlkPerTile) {
+    kloop(IC<NT>{});
+  } else {
+    auto pick = [&](auto v) {
+      if (split_nt == decltype(v)::value + 1) kloop(IC<decltype(v)::value + 1>{});
+    };
+    SFor<0, NT>::run(pick);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < kLag; ++j) {
+    const int u = kT - kLag + j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[tmt(u)][tnt(u)][r] = fmaf(pend[j][r], pend_s[j], acc[tmt(u)][tnt(u)][r]);
+  }
 
   const int row_w = m0 + wm * (TM / WM) + li;  // + mt * 16: the lane's output row
   const int col_w = n0 + wn * (TN / WN) + 4 * g;  // + nt * 16: the lane's first output column
