@@ -568,10 +568,8 @@ __device__ __forceinline__ void moe_item(const MoeGemmArgs& p, uint8_t* smem, in
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const f32x4 xv = acc[mt][nt], yv = acc[mt][nt + 1];
-          const uint32_t x0 = f32_to_bf16_bits(xv[0]) | (f32_to_bf16_bits(xv[1]) << 16);
-          const uint32_t x1 = f32_to_bf16_bits(xv[2]) | (f32_to_bf16_bits(xv[3]) << 16);
-          const uint32_t y0 = f32_to_bf16_bits(yv[0]) | (f32_to_bf16_bits(yv[1]) << 16);
-          const uint32_t y1 = f32_to_bf16_bits(yv[2]) | (f32_to_bf16_bits(yv[3]) << 16);
+          const uint32_t x0 = pack_bf16x2(xv[0], xv[1]), x1 = pack_bf16x2(xv[2], xv[3]);
+          const uint32_t y0 = pack_bf16x2(yv[0], yv[1]), y1 = pack_bf16x2(yv[2], yv[3]);
           const auto s0 = __builtin_amdgcn_permlane16_swap(x0, y0, false, false);
           const auto s1 = __builtin_amdgcn_permlane16_swap(x1, y1, false, false);
           const u32x4 v = {s0[0], s1[0], s0[1], s1[1]};
@@ -634,7 +632,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     }
     u32x4 o;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = f32_to_bf16_bits(acc[2 * i]) | (f32_to_bf16_bits(acc[2 * i + 1]) << 16);
+    for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(acc[2 * i], acc[2 * i + 1]);
     *reinterpret_cast<u32x4*>(out + (int64_t)t * D + c0) = o;
   }
 }
