@@ -475,6 +475,20 @@ __device__ __forceinline__ void moe_item(const MoeGemmArgs& p, uint8_t* smem, in
 
     const int swz_lo = (g ^ (li & 7)) << 4, swz_hi = ((4 + g) ^ (li & 7)) << 4;
     const int a_row = (wm * (TM / 2) + li) * 128, b_row = (wn * 64 + li) * 128;
+    // The dense LDS kernel's step (gemm_a8w8.hip): the smaller fragment set held, the other streamed
+    // one tile ahead, and each MFMA's fold kLag MFMAs after it (bitwise the same sums).
+    constexpr int kLag = 3, kT = MT * NT;
+    constexpr bool kHoldA = MT <= NT;
+    constexpr int kHeld = kHoldA ? MT : NT, kStreamed = kHoldA ? NT : MT;
+    auto tmt = [](int t) { return kHoldA ? t % MT : t / NT; };
+    auto tnt = [](int t) { return kHoldA ? t / MT : t % NT; };
+    f32x4 pend[kLag];
+    float pend_s[kLag];
+#pragma unroll
+    for (int j = 0; j < kLag; ++j) {
+      pend[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      pend_s[j] = 0.f;
+    }
     auto compute = [&](int kb, int st) {
       const uint8_t* A = sA + st * kStageA;
       const uint8_t* B = sB + st * kStageB;
@@ -486,25 +500,55 @@ __device__ __forceinline__ void moe_item(const MoeGemmArgs& p, uint8_t* smem, in
       } else {
         sbv[0] = sbv[1] = sSB[wn >> 1][kb];
       }
-      i32x8 bf[NT];
+      auto read_a = [&](int mt) {
+        return cat(*reinterpret_cast<const u32x4*>(A + a_row + swz_lo + mt * 2048),
+                   *reinterpret_cast<const u32x4*>(A + a_row + swz_hi + mt * 2048));
+      };
+      auto read_b = [&](int nt) {
+        return cat(*reinterpret_cast<const u32x4*>(B + b_row + swz_lo + nt * 2048),
+                   *reinterpret_cast<const u32x4*>(B + b_row + swz_hi + nt * 2048));
+      };
+      i32x8 held[kHeld];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        bf[nt] = cat(*reinterpret_cast<const u32x4*>(B + b_row + swz_lo + nt * 2048),
-                     *reinterpret_cast<const u32x4*>(B + b_row + swz_hi + nt * 2048));
+      for (int i = 0; i < kHeld; ++i) held[i] = kHoldA ? read_a(i) : read_b(i);
+      float s0[MT], s1[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const i32x8 af = cat(*reinterpret_cast<const u32x4*>(A + a_row + swz_lo + mt * 2048),
-                             *reinterpret_cast<const u32x4*>(A + a_row + swz_hi + mt * 2048));
         const float sa = SA[mt * 16];
-        const float s0 = sa * sbv[0], s1 = sa * sbv[1];
+        s0[mt] = sa * sbv[0];
+        s1[mt] = sa * sbv[1];
+      }
+      i32x8 cur, nxt = kHoldA ? read_b(0) : read_a(0);
+      f32x4 part[kT];
+      float sc[kT];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-          const f32x4 part = mfma16x128<0>(bf[nt], af, z);  // lane: row li, columns 4g..4g+3
-          const float s = (nt & 1) ? s1 : s0;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(part[r], s, acc[mt][nt][r]);
+      for (int t = 0; t < kT; ++t) {
+        const int mt = tmt(t), nt = tnt(t);
+        const int si = t / kHeld, hi = t % kHeld;
+        if (hi == 0) {
+          cur = nxt;
+          if (si + 1 < kStreamed) nxt = kHoldA ? read_b(si + 1) : read_a(si + 1);
         }
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        // lane: row li, columns 4g..4g+3 (the weight is the first operand)
+        part[t] = kHoldA ? mfma16x128<0>(cur, held[hi], z) : mfma16x128<0>(held[hi], cur, z);
+        sc[t] = (nt & 1) ? s1[mt] : s0[mt];
+        if (t >= kLag) {
+          const int u = t - kLag;
+          asm volatile("" : "+v"(part[u]) : "v"(part[t]));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[tmt(u)][tnt(u)][r] = fmaf(part[u][r], sc[u], acc[tmt(u)][tnt(u)][r]);
+        } else {
+          const int u = kT - kLag + t;
+          asm volatile("" : "+v"(pend[t]) : "v"(part[t]));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[tmt(u)][tnt(u)][r] = fmaf(pend[t][r], pend_s[t], acc[tmt(u)][tnt(u)][r]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kLag; ++j) {
+        pend[j] = part[kT - kLag + j];
+        pend_s[j] = sc[kT - kLag + j];
       }
     };
 
@@ -520,6 +564,12 @@ __device__ __forceinline__ void moe_item(const MoeGemmArgs& p, uint8_t* smem, in
       st_fill = st_fill + 1 == S ? 0 : st_fill + 1;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < kLag; ++j) {
+      const int u = kT - kLag + j;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[tmt(u)][tnt(u)][r] = fmaf(pend[j][r], pend_s[j], acc[tmt(u)][tnt(u)][r]);
+    }
 
     if (MODE == kGateUp) {
       // h = bf16(silu(gate) * up), kept in the gate tiles' registers; per row, e4m3 at scale
