@@ -22,6 +22,12 @@ __device__ __forceinline__ void nt_store8(uint8_t* p, uint32_t a, uint32_t b) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x2*>(p));
 }
 
+// NT_LOAD: x streams past the caches (large inputs, read once). Small inputs, a decode step's
+// activations, load through them: they are usually still cached from the write that made them (measured
+// on the decode step: 0.2920 -> 0.2885 ms; at T = 2048 and 16384, H = 7168 the non-temporal loads are
+// 4% faster).
+constexpr int64_t kQuantCachedLoadBytes = 8ll << 20;
+template <bool NT_LOAD>
 __global__ __launch_bounds__(256) void quant_fp8_1x128_kernel(const uint16_t* __restrict__ x, int64_t xs,
                                                               uint8_t* __restrict__ q, float* __restrict__ scales,
                                                               int64_t rows, int64_t cols) {
@@ -38,8 +44,8 @@ __global__ __launch_bounds__(256) void quant_fp8_1x128_kernel(const uint16_t* __
   u32x4 v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
   const uint16_t* src = x + row * xs + g * 128;
   if (active) {
-    v0 = ld16_nt(src + 8 * j);
-    v1 = ld16_nt(src + 64 + 8 * j);
+    v0 = NT_LOAD ? ld16_nt(src + 8 * j) : ld16(src + 8 * j);
+    v1 = NT_LOAD ? ld16_nt(src + 64 + 8 * j) : ld16(src + 64 + 8 * j);
   }
   float f[16];
   const uint32_t w[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
@@ -258,8 +264,12 @@ extern "C" int aklr_per_group_quant_fp8(const void* x, int64_t x_row_stride, voi
   const int64_t blocks = (n_tokens + 7) / 8 * ((groups + 3) / 4);
   if (blocks > 0x7FFFFFFF) return AKLR_ERR_INVALID_ARGUMENT;
   const dim3 grid((unsigned)blocks);
-  hipLaunchKernelGGL(quant_fp8_1x128_kernel, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(x),
-                     x_row_stride, static_cast<uint8_t*>(quantized), scales, n_tokens, hidden_size);
+  if (n_tokens * hidden_size * 2 > kQuantCachedLoadBytes)
+    hipLaunchKernelGGL(quant_fp8_1x128_kernel<true>, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(x),
+                       x_row_stride, static_cast<uint8_t*>(quantized), scales, n_tokens, hidden_size);
+  else
+    hipLaunchKernelGGL(quant_fp8_1x128_kernel<false>, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(x),
+                       x_row_stride, static_cast<uint8_t*>(quantized), scales, n_tokens, hidden_size);
   AKLR_LAUNCH_CHECK();
   return AKLR_OK;
 }
