@@ -1323,3 +1323,54 @@ extern "C" int aklr_quant_gemm_a8w8_blockscale(const void* x, int64_t ldx, const
   AKLR_LAUNCH_CHECK();
   return AKLR_OK;
 }
+
+// ---------------------------------------------------------------------------------------------
+// b given as (k, n) (trans_b = false): dst[c][r] = src[r][c] over bytes, so the GEMM entries read it
+// as (n, k). A 256-thread workgroup moves a 64 x 64 byte tile through LDS: lane t loads 16 bytes of
+// source row t / 4, then gathers the 16 bytes of destination row t / 4 from the tile's column and
+// stores them as one 16-byte write. Rows of the LDS tile are 68 bytes apart (4-byte aligned, and the
+// column gather spreads over banks).
+namespace aklr {
+__global__ __launch_bounds__(256) void transpose_b8_kernel(const uint8_t* __restrict__ src, int64_t rows,
+                                                           int64_t cols, int64_t src_ld, uint8_t* __restrict__ dst,
+                                                           int64_t dst_ld) {
+  constexpr int kPitch = 68;
+  __shared__ uint8_t tile[64 * kPitch];
+  const int64_t tiles_c = (cols + 63) / 64;
+  const int64_t r0 = (int64_t)(blockIdx.x / tiles_c) * 64, c0 = (int64_t)(blockIdx.x % tiles_c) * 64;
+  const int t = threadIdx.x, tr = t >> 2, tc = (t & 3) * 16;
+  u32x4 v = {0, 0, 0, 0};
+  if (r0 + tr < rows && c0 + tc < cols) v = *reinterpret_cast<const u32x4*>(src + (r0 + tr) * src_ld + c0 + tc);
+  uint32_t* row = reinterpret_cast<uint32_t*>(&tile[tr * kPitch + tc]);
+  row[0] = v.x;
+  row[1] = v.y;
+  row[2] = v.z;
+  row[3] = v.w;
+  __syncthreads();
+  // destination row c0 + tr (a source column), bytes from source rows r0 + tc .. + 15
+  if (c0 + tr >= cols || r0 + tc >= rows) return;
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t x = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) x |= (uint32_t)tile[(tc + 4 * i + b) * kPitch + tr] << (8 * b);
+    w[i] = x;
+  }
+  *reinterpret_cast<u32x4*>(dst + (c0 + tr) * dst_ld + r0 + tc) = u32x4{w[0], w[1], w[2], w[3]};
+}
+}  // namespace aklr
+
+extern "C" int aklr_transpose_b8(const void* src, int64_t rows, int64_t cols, int64_t src_ld, void* dst,
+                                 int64_t dst_ld, hipStream_t stream) {
+  if (!src || !dst) return AKLR_ERR_INVALID_ARGUMENT;
+  if (rows <= 0 || cols <= 0 || rows % 16 != 0 || cols % 16 != 0) return AKLR_ERR_INVALID_ARGUMENT;
+  if (src_ld < cols || dst_ld < rows || src_ld % 16 != 0 || dst_ld % 16 != 0) return AKLR_ERR_INVALID_ARGUMENT;
+  if (!aklr_aligned16(src) || !aklr_aligned16(dst)) return AKLR_ERR_INVALID_ARGUMENT;
+  const int64_t blocks = ((rows + 63) / 64) * ((cols + 63) / 64);
+  if (blocks > 0x7FFFFFFF) return AKLR_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(aklr::transpose_b8_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     static_cast<const uint8_t*>(src), rows, cols, src_ld, static_cast<uint8_t*>(dst), dst_ld);
+  AKLR_LAUNCH_CHECK();
+  return AKLR_OK;
+}

@@ -9,6 +9,8 @@
                                  bytes per_group_quant_fp8 writes; also accepted as a (1, m)-strided view);
     b_shuffled_row_major_a_scale "none:preshuffled", a_scale.is_row_major = True.
   Constraint (contract.py:242-246): the shuffled variants take trans_b, K-major scales, no bias, e4m3.
+  trans_b = False (row_major; b is (k, n), contract.py:61-76): b is transposed on the GPU into (n, k)
+  scratch (aklr_transpose_b8), then the same GEMM runs.
 ``gemm_a4w4_mxfp4`` -- aklr/ops/gemm/api.py:49-63, contract aklr/ops/gemm/contract.py:315-390:
     out = alpha * (a * 2^(a_scale-127)) @ (b * 2^(b_scale-127))^T + bias, alpha = 1, beta = 0, NT only.
   Variants: row_major ("none:none") and b_shuffled ("none:preshuffled", the default): preshuffled b and
@@ -16,8 +18,7 @@
 
 Calls the kernels do not serve return a ``FallbackReason`` (never raise): outside the contract ->
 OUT_OF_CONTRACT (the in-contract rules of aklr/core/contract/fastkey/_fast_key_fn.py: dtypes, shapes,
-strides, 16-byte alignment, one device, no output/input overlap); in the contract but in a layout no
-kernel here implements (trans_b=False) -> NO_WORKLOAD.
+strides, 16-byte alignment, one device, no output/input overlap).
 """
 from __future__ import annotations
 
@@ -79,16 +80,22 @@ class _Gemm8Plan:
     b_layout: int
     variant: str
     kernel_ref: str = field(default="")
+    transpose_b: bool = False  # b is (k, n): transposed into (n, k) scratch first
 
 
 def _run_gemm8(p: _Gemm8Plan):
     dev = p.a.device
     out = p.out if p.out is not None else torch.empty((p.m, p.n), dtype=p.out_dtype, device=dev)
     L = _lib.lib()
+    b = p.b
+    if p.transpose_b:
+        b = torch.empty((p.n, p.k), dtype=p.b.dtype, device=dev)
+        _lib.check(L.aklr_transpose_b8(p.b.data_ptr(), p.k, p.n, p.b.stride(0), b.data_ptr(), p.k, _stream(dev)),
+                   "gemm_a8w8_blockwise_scaled (b transpose)")
     ws_bytes = L.aklr_gemm_a8w8_blockscale_workspace_bytes(p.m, p.n, p.k)
     ws = workspace.get(dev, ws_bytes)
     st = L.aklr_gemm_a8w8_blockscale(
-        p.a.data_ptr(), p.a.stride(0), p.b.data_ptr(), p.b.stride(0) if p.b_layout == _lib.B_ROW_MAJOR else p.k,
+        p.a.data_ptr(), p.a.stride(0), b.data_ptr(), b.stride(0) if p.b_layout == _lib.B_ROW_MAJOR else p.k,
         p.a_scale.data_ptr(), p.sa_sm, p.sa_sk, p.b_scale.data_ptr(), p.b_scale.stride(0),
         p.bias.data_ptr() if p.bias is not None else None, out.data_ptr(), out.stride(0), p.m, p.n, p.k,
         _FP8[p.a.dtype], p.b_layout, _OUT[p.out_dtype], ws.data_ptr() if ws is not None else None, ws_bytes,
@@ -180,12 +187,13 @@ def gemm_a8w8_blockwise_scaled(
         return _OOC
     if not _out_ok(out, m, n, dt, a.device, (a, b, a_scale, b_scale, bias)):
         return _OOC
-    if not trans_b:
-        return FallbackReason.NO_WORKLOAD
     b_layout = _lib.B_ROW_MAJOR if variant == "row_major" else _lib.B_PRESHUFFLE_16x16
     path = "stream" if m <= 128 else "lds"  # the library picks the same way (kStreamMaxM)
-    return _Gemm8Plan(a, b, a_scale, b_scale, bias, out, dt, m, n, k, sa_sm, sa_sk, b_layout, variant,
-                      f"aklr_gemm_a8w8_blockscale:{path}")
+    # trans_b = False (row_major only, by the check above): b is (k, n), as the reference's _weight
+    # transposes it (aklr/ops/gemm/reference.py:32-37)
+    ref = f"aklr_gemm_a8w8_blockscale:{path}" if trans_b else f"aklr_transpose_b8+aklr_gemm_a8w8_blockscale:{path}"
+    return _Gemm8Plan(a, b, a_scale, b_scale, bias, out, dt, m, n, k, sa_sm, sa_sk, b_layout, variant, ref,
+                      transpose_b=not trans_b)
 
 
 # ---------------------------------------------------------------------------------------------

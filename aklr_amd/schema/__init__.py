@@ -72,7 +72,7 @@ CONTRACTS: dict[str, Contract] = {
             "b_shuffled_row_major_a_scale": {"b_preshuffled": True, "a_scale_column_major": False},
         },
         ("a", "b", "a_scale", "b_scale", "scale_major_mode", "trans_b", "operand_format", "bias", "out_dtype", "out"),
-        ("out",), {"trans_b": (True,)}),
+        ("out",), {"trans_b": (True, False)}),  # trans_b = False: row_major only (contract.py:242-246)
     # aklr/ops/gemm/contract.py:315-390
     "gemm_a4w4_mxfp4@1.0": Contract(
         "gemm_a4w4_mxfp4.hip", ("gemm_a4w4.hip", "quant.hip"),

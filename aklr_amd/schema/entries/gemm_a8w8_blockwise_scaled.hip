@@ -8,8 +8,9 @@
 // order by the last workgroup to arrive). m > 128: 256 x 256 down to 128 x 128 workgroup tiles through
 // a 2- to 4-stage LDS ring filled by direct-to-LDS loads, XCD-aware tile order. Results are bitwise
 // reproducible. b is row-major or aiter's 16 x 16 shuffle_weight layout; the layout variant
-// (variant.h) says how a_scale is stored. Kernels: aklr_amd/csrc/gemm_a8w8.hip through
-// aklr_gemm_a8w8_blockscale.
+// (variant.h) says how a_scale is stored. A row-major b given as (k, n) (trans_b = false) is first
+// transposed into (n, k) scratch of this call. Kernels: aklr_amd/csrc/gemm_a8w8.hip through
+// aklr_transpose_b8 and aklr_gemm_a8w8_blockscale.
 #include "entry.h"
 #include "variant.h"
 
@@ -18,15 +19,16 @@ namespace {
 void run(const at::Tensor& a, const at::Tensor& b, const at::Tensor& a_scale, const at::Tensor& b_scale,
          c10::string_view scale_major_mode, bool trans_b, c10::string_view operand_format,
          const std::optional<at::Tensor>& bias, std::optional<at::ScalarType> out_dtype, at::Tensor& out) {
-  TORCH_CHECK(trans_b, "gemm_a8w8_blockwise_scaled: b must be (n, k)");
+  TORCH_CHECK(trans_b || !aklr_variant::b_preshuffled, "gemm_a8w8_blockwise_scaled: a shuffled b is (n, k)");
   TORCH_CHECK(operand_format == (aklr_variant::b_preshuffled ? "none:preshuffled" : "none:none"),
               "gemm_a8w8_blockwise_scaled: operand_format does not match the layout variant");
   TORCH_CHECK(a.dim() == 2 && b.dim() == 2 && a.is_contiguous() && b.is_contiguous(), "a, b: 2-d, contiguous");
   const at::ScalarType fp8 = a.scalar_type();
   TORCH_CHECK((fp8 == at::kFloat8_e4m3fn || fp8 == at::kFloat8_e5m2) && b.scalar_type() == fp8,
               "a, b: one fp8 dtype");
-  const int64_t m = a.size(0), k = a.size(1), n = b.size(0), kb = k / 128;
-  TORCH_CHECK(b.size(1) == k && k % 128 == 0 && n % 16 == 0, "b: (n, k), k % 128 == 0, n % 16 == 0");
+  const int64_t m = a.size(0), k = a.size(1), n = trans_b ? b.size(0) : b.size(1), kb = k / 128;
+  TORCH_CHECK((trans_b ? b.size(1) : b.size(0)) == k && k % 128 == 0 && n % 16 == 0,
+              "b: (n, k), or (k, n) when not trans_b; k % 128 == 0, n % 16 == 0");
   const bool mn = scale_major_mode == "MN";
   TORCH_CHECK(mn || scale_major_mode == "K", "scale_major_mode: K or MN");
   // element (i, kb) of a_scale at i * sm + kb * sk
@@ -49,10 +51,16 @@ void run(const at::Tensor& a, const at::Tensor& b, const at::Tensor& a_scale, co
   TORCH_CHECK((od == at::kBFloat16 || od == at::kHalf) && (!out_dtype.has_value() || *out_dtype == od),
               "out: bf16 or fp16, of out_dtype when one is given");
   TORCH_CHECK(out.dim() == 2 && out.size(0) == m && out.size(1) == n && out.stride(1) == 1, "out: [m, n]");
+  at::Tensor bt = b;  // (n, k)
+  if (!trans_b) {
+    bt = at::empty({n, k}, b.options());
+    aklr_entry::check(aklr_transpose_b8(b.data_ptr(), k, n, b.stride(0), bt.data_ptr(), k, aklr_entry::stream_of(a)),
+                      "gemm_a8w8_blockwise_scaled (b transpose)");
+  }
   const size_t ws_bytes = aklr_gemm_a8w8_blockscale_workspace_bytes(m, n, k);
   at::Tensor ws = aklr_entry::scratch(a, ws_bytes);
   aklr_entry::check(
-      aklr_gemm_a8w8_blockscale(a.data_ptr(), a.stride(0), b.data_ptr(), aklr_variant::b_preshuffled ? k : b.stride(0),
+      aklr_gemm_a8w8_blockscale(a.data_ptr(), a.stride(0), bt.data_ptr(), aklr_variant::b_preshuffled ? k : bt.stride(0),
                                 a_scale.data_ptr<float>(), sm, sk, b_scale.data_ptr<float>(), b_scale.stride(0),
                                 bias_ptr, out.data_ptr(), out.stride(0), m, n, k,
                                 fp8 == at::kFloat8_e5m2 ? AKLR_FP8_E5M2 : AKLR_FP8_E4M3FN,

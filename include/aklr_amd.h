@@ -135,6 +135,18 @@ int aklr_gemm_a8w8_blockscale_noalloc(const void* a, int64_t lda, const void* b,
                                       int fp8_dtype, int b_layout, int out_dtype, hipStream_t stream);
 
 /*
+ * Byte transpose dst[c][r] = src[r][c] for a [rows, cols] matrix of 8-bit codes (row strides src_ld,
+ * dst_ld in bytes). It serves gemm_a8w8_blockwise_scaled with trans_b = false, where b is (k, n)
+ * (aklr/ops/gemm/contract.py:61-76 `_TRANS_B`, aklr/ops/gemm/reference.py:32-37 `_weight`: b.mT): the
+ * host side transposes b into (n, k) scratch of its own and calls aklr_gemm_a8w8_blockscale. No kernel
+ * ABI of the reference corresponds to it (none of its recorded kernels takes trans_b = false).
+ * rows % 16 == 0, cols % 16 == 0; pointers 16-byte aligned; src_ld >= cols and dst_ld >= rows,
+ * multiples of 16.
+ */
+int aklr_transpose_b8(const void* src, int64_t rows, int64_t cols, int64_t src_ld, void* dst, int64_t dst_ld,
+                      hipStream_t stream);
+
+/*
  * Per-1x128 FP8 quantization of bf16 activations fused into the block-scaled FP8 GEMM:
  * out = GEMM(per_group_quant_fp8(x), b), equal bit for bit to aklr_per_group_quant_fp8 followed by
  * aklr_gemm_a8w8_blockscale on its codes and group-major scales (e4m3fn).

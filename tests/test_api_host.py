@@ -122,8 +122,13 @@ def test_gemm8_out_of_contract(as_gpu):
     aa = big[: 4 * 256].view(torch.float8_e4m3fn).view(4, 256)
     oo = big[:4 * 144 * 2].view(torch.bfloat16).view(4, 144)
     assert api(aa, b, sa, sb, out=oo) is FR.OUT_OF_CONTRACT
-    # trans_b=False is in the contract, served by no kernel here
-    assert api(a, fp8((256, 144)), sa, sb, trans_b=False) is FR.NO_WORKLOAD
+    # trans_b=False (b as (k, n)) is served on row_major: b transposed first, then the same GEMM
+    plan = api(a, fp8((256, 144)), sa, sb, trans_b=False)
+    assert not isinstance(plan, FR) and plan.kernel_ref.startswith("aklr_transpose_b8+aklr_gemm_a8w8_blockscale")
+    assert api(a, fp8((144, 256)), sa, sb, trans_b=False) is FR.OUT_OF_CONTRACT  # (n, k) given for (k, n)
+    # the shuffled variants take trans_b only (contract.py:242-246)
+    assert api(a, layouts.shuffle_weight(fp8((144, 256))), layouts.column_major(sa), sb, trans_b=False,
+               operand_format="none:preshuffled") is FR.OUT_OF_CONTRACT
 
 
 def test_gemm4_variants(as_gpu):

@@ -92,6 +92,51 @@ def test_config1():
     _run_and_check(32, 1024, 2048, rows=32, cols=1024)
 
 
+# trans_b=False (row_major): b given as (k, n); the op transposes it on the GPU, then runs the GEMM.
+# Checked against the oracle on the (n, k) weight, and bit for bit against trans_b=True on b.T.
+@pytest.mark.parametrize("m,n,k,mode,bias,fp16,e5", [
+    (1, 2112, 7168, "K", False, False, False),     # stream kernel, split K
+    (64, 1040, 2048, "MN", True, True, False),     # n not a multiple of the 64-byte transpose tile
+    (300, 1536, 1024, "K", True, False, True),     # LDS kernel, e5m2
+])
+def test_trans_b_false(m, n, k, mode, bias, fp16, e5):
+    dtype = torch.float8_e5m2 if e5 else torch.float8_e4m3fn
+    say(f"gemm_a8w8 trans_b=False m={m} n={n} k={k} mode={mode} bias={bias} fp16={fp16} {_fmt(dtype)}")
+    q, s, b, bs = _fp8_inputs(m, n, k, seed=m + 5, dtype=dtype)
+    bias_t = torch.randn(n, device=DEV, generator=workloads.generator(m, DEV)) if bias else None
+    a_scale = s.t().contiguous() if mode == "K" else s
+    out_dtype = torch.float16 if fp16 else None
+    b_kn = b.t().contiguous()  # (k, n)
+    out = aklr_amd.gemm_a8w8_blockwise_scaled(q, b_kn, a_scale, bs, scale_major_mode=mode, trans_b=False,
+                                              bias=bias_t, out_dtype=out_dtype)
+    assert isinstance(out, torch.Tensor), f"not served: {out}"
+    want = aklr_amd.gemm_a8w8_blockwise_scaled(q, b, a_scale, bs, scale_major_mode=mode, bias=bias_t,
+                                               out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16)), "trans_b=False differs from trans_b=True on b.T"
+    r, c = _sample(m, n, 64, 512, m)
+    ref = ogemm.gemm_a8w8_blockwise_scaled(u8(q), u8(b), s.cpu().numpy(), bs.cpu().numpy(), fmt=_fmt(dtype),
+                                           scale_major_mode="MN", bias=None if bias_t is None else f32(bias_t),
+                                           rows=r, cols=c)
+    _check(f32(out)[np.ix_(r, c)], ref, f"trans_b=False m={m} n={n} k={k}",
+           out_dtype="float16" if fp16 else "bfloat16")
+
+
+def test_transpose_b8_exact():
+    # the byte transpose itself, through the C ABI, on a ragged (k, n) with a padded source stride
+    from aklr_amd import _lib
+    L = _lib.lib()
+    g = workloads.generator(3, DEV)
+    rows, cols, ld = 272, 1040, 1072
+    src = torch.randint(0, 256, (rows, ld), dtype=torch.uint8, device=DEV, generator=g)
+    dst = torch.full((cols, rows), 7, dtype=torch.uint8, device=DEV)
+    st = L.aklr_transpose_b8(src.data_ptr(), rows, cols, ld, dst.data_ptr(), rows,
+                             torch.cuda.current_stream().cuda_stream)
+    assert st == 0, L.aklr_status_string(st)
+    torch.cuda.synchronize()
+    assert torch.equal(dst, src[:, :cols].t())
+
+
 @pytest.mark.parametrize("nk", workloads.DEEPSEEK_NK)
 @pytest.mark.parametrize("m", workloads.DECODE_M)
 def test_decode_row_major(m, nk):

@@ -103,6 +103,21 @@ def test_gemm_a8w8_row_major_package(mode, m, n, k):
     assert _same(out, ref)
 
 
+@pytest.mark.parametrize("m,n,k", [(8, 4096, 1536), (512, 2048, 2048)])
+def test_gemm_a8w8_row_major_package_b_kn(m, n, k):
+    # trans_b = False: b as (k, n), transposed by the package into its own scratch
+    say(f"schema gemm_a8w8 row_major trans_b=False m={m} n={n} k={k}")
+    op = _op("gemm_a8w8_blockwise_scaled@1.0", "row_major")
+    q, s, b, bs = _fp8_operands(m, n, k, seed=m + 9)
+    a_scale = s.t().contiguous()
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    op(a=q, b=b.t().contiguous(), a_scale=a_scale, b_scale=bs, scale_major_mode="K", trans_b=False,
+       operand_format="none:none", bias=None, out_dtype=None, out=out)
+    ref = aklr_amd.gemm_a8w8_blockwise_scaled(q, b, a_scale, bs)
+    torch.cuda.synchronize()
+    assert _same(out, ref)
+
+
 @pytest.mark.parametrize("m,n,k", [(4, 2112, 7168), (200, 1024, 4096)])
 def test_gemm_a4w4_b_shuffled_package(m, n, k):
     say(f"schema gemm_a4w4 b_shuffled m={m} n={n} k={k}")

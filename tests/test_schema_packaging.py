@@ -278,7 +278,9 @@ def test_fill_refuses_what_it_has_no_kernel_for():
     with pytest.raises(S.PackagingError, match="layout variant"):
         S.fill(_definition(variant="b_preshuffled_32x32"))
     with pytest.raises(S.PackagingError, match="trans_b"):
-        S.fill(_definition(variant="row_major", attrs={"trans_b": False}))
+        S.fill(_definition("gemm_a4w4_mxfp4@1.0", "row_major", attrs={"trans_b": False}))
+    # the FP8 GEMM's row_major kernel takes b as (k, n) too
+    assert S.fill(_definition(variant="row_major", attrs={"trans_b": False}))["kernel"]["language"] == "hip"
     with pytest.raises(S.PackagingError, match="scoring_func"):
         S.fill(_definition("deepseek_v2_fp8_moe@1.0", "shuffled_16x16", attrs={"scoring_func": "softmax"}))
     d = _definition()
