@@ -35,6 +35,7 @@ struct Gemm8Args {
   int64_t ldo;
   int m, n, k;
   int out_dtype;
+  int nt_out;          // lds kernel: output stores are non-temporal
   uint64_t* counters;  // when splits > 1: one arrival word per output tile (launch-tagged)
   float* partial;      // when splits > 1: per 16x16 tile, in accumulator order
   int splits;
@@ -770,7 +771,6 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
     for (int r = 0; r < 4; ++r) acc[tmt(u)][tnt(u)][r] = fmaf(pend[j][r], pend_s[j], acc[tmt(u)][tnt(u)][r]);
   }
 
-  const int row_w = m0 + wm * (TM / WM) + li;  // + mt * 16: the lane's output row
   const int col_w = n0 + wn * (TN / WN) + 4 * g;  // + nt * 16: the lane's first output column
   if (p.splits > 1) {
     // partials in accumulator order, [split][tile][wave][mt][nt][lane] x 4 fp32: the workgroup that
@@ -818,52 +818,61 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
     }
   }
 
-  // Output: for each pair of column tiles (nt, nt + 1) a lane packs its 4 columns of each into two
-  // words, and permlane16_swap exchanges the odd lane groups of the first with the even lane groups
-  // of the second: lane group g then holds columns 8 * (g / 2) .. + 7 of tile nt + (g & 1).
-  const int col_s = n0 + wn * (TN / WN) + (g & 1) * 16 + (g >> 1) * 8;  // + nt * 16 (nt even)
+  // Output through LDS, whose ring is free once every wave has left the K loop. Rows [0, TM/2) of the
+  // tile go to sA's bytes and rows [TM/2, TM) to sB's, as rows of TN * 2 bytes whose 16-byte chunks
+  // are XOR-swizzled by row; then each thread moves 16-byte chunks to memory, so that a wave stores
+  // 1 KiB of whole tile rows (full 128-byte lines) per instruction. A lane's own fragments would
+  // store 64 bytes per row, two halves of a line from two instructions.
+  constexpr int kCpr = TN / 8;  // 16-byte chunks per tile row
+  constexpr int kSwz = (kCpr & -kCpr) < 8 ? (kCpr & -kCpr) : 8;  // XOR range; divides kCpr
+  constexpr int kHalfRows = TM / 2;
+  static_assert(kHalfRows * TN * 2 <= S * kStageA && kHalfRows * TN * 2 <= S * kStageB, "output staging");
+  static_assert(kHalfRows * kCpr % 512 == 0 && WM % 2 == 0, "output staging");
+  __syncthreads();  // every wave's last fragment reads are done
+  {
+    uint8_t* const half = wm < WM / 2 ? sA : sB;
+    const int r0 = (wm % (WM / 2)) * (TM / WM) + li;  // + mt * 16: the lane's row within its half
 #pragma unroll
-  for (int nt = 0; nt + 1 < NT; nt += 2) {
-    f32x4 bx = {0.f, 0.f, 0.f, 0.f}, by = {0.f, 0.f, 0.f, 0.f};
-    if (p.bias) {
-      const int cx = min(col_w + nt * 16, p.n - 4), cy = min(col_w + nt * 16 + 16, p.n - 4);
+    for (int nt = 0; nt < NT; ++nt) {
+      f32x4 bx = {0.f, 0.f, 0.f, 0.f};
+      if (p.bias) {
+        const int cx = min(col_w + nt * 16, p.n - 4);  // columns past n are computed, never stored
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        bx[r] = p.bias[cx + r];
-        by[r] = p.bias[cy + r];
+        for (int r = 0; r < 4; ++r) bx[r] = p.bias[cx + r];
+      }
+      const int ch = (wn * (TN / WN) + nt * 16) / 8 + (g >> 1);  // the lane's columns 4g..4g+3
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const f32x4 x = acc[mt][nt] + bx;
+        const u32x2 v = {pack_out2(x[0], x[1], p.out_dtype), pack_out2(x[2], x[3], p.out_dtype)};
+        const int r = r0 + mt * 16;
+        *reinterpret_cast<u32x2*>(half + r * (TN * 2) + (ch ^ (r & (kSwz - 1))) * 16 + (g & 1) * 8) = v;
       }
     }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const f32x4 x = acc[mt][nt] + bx, y = acc[mt][nt + 1] + by;
-      const uint32_t x0 = pack_out2(x[0], x[1], p.out_dtype), x1 = pack_out2(x[2], x[3], p.out_dtype);
-      const uint32_t y0 = pack_out2(y[0], y[1], p.out_dtype), y1 = pack_out2(y[2], y[3], p.out_dtype);
-      const auto s0 = __builtin_amdgcn_permlane16_swap(x0, y0, false, false);
-      const auto s1 = __builtin_amdgcn_permlane16_swap(x1, y1, false, false);
-      const u32x4 v = {s0[0], s1[0], s0[1], s1[1]};
-      const int row = row_w + mt * 16, col = col_s + nt * 16;
-      if (row < p.m && col < p.n)
-        *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + col) = v;
-    }
   }
-  if constexpr (NT % 2 == 1) {
-    // the odd last column tile: each lane stores its 4 columns as 8 bytes
-    constexpr int nt = NT - 1;
-    const int col = col_w + nt * 16;
-    f32x4 bx = {0.f, 0.f, 0.f, 0.f};
-    if (p.bias && col < p.n) {
+  __syncthreads();
+  constexpr int kHalfIters = kHalfRows * kCpr / 512;
+  auto store_rows = [&](auto nt_c) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) bx[r] = p.bias[col + r];
+    for (int it = 0; it < 2 * kHalfIters; ++it) {
+      const int idx = (it % kHalfIters) * 512 + (int)threadIdx.x;
+      const int r = idx / kCpr, ch = idx % kCpr;
+      const uint8_t* const half = it < kHalfIters ? sA : sB;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(half + r * (TN * 2) + (ch ^ (r & (kSwz - 1))) * 16);
+      const int row = m0 + (it < kHalfIters ? 0 : kHalfRows) + r, col = n0 + ch * 8;
+      if (row < p.m && col < p.n) {  // n % 16 == 0: a chunk is wholly inside or past n
+        u32x4* const dst = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + col);
+        if constexpr (decltype(nt_c)::value)
+          __builtin_nontemporal_store(v, dst);
+        else
+          *dst = v;
+      }
     }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const f32x4 x = acc[mt][nt] + bx;
-      const u32x2 v = {pack_out2(x[0], x[1], p.out_dtype), pack_out2(x[2], x[3], p.out_dtype)};
-      const int row = row_w + mt * 16;
-      if (row < p.m && col < p.n)
-        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + col) = v;
-    }
-  }
+  };
+  if (p.nt_out)
+    store_rows(IC<1>{});
+  else
+    store_rows(IC<0>{});
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1065,6 +1074,14 @@ static Plan8 plan8(int64_t m, int64_t n, int64_t k, bool fill = true) {
   return plan8_lds_best(m, n, k);
 }
 
+// The LDS kernel's output stores are non-temporal unless the output's row pitch is 8 or 16 KiB.
+// Measured on cold b_shuffled operands (us, cached -> non-temporal stores, both whole lines): 64 KiB
+// pitch (n = 32768, k = 1024) 250 -> 190 at m = 4096 and 107 -> 100 at m = 2048; 48 KiB (24576 x 1536)
+// 195 -> 176-183; 32 KiB at m = 8192 (k = 1024) 229 -> 181; 14 KiB (7168 x 2048) 70.9 -> 68.8; 6 KiB
+// (3072 x 1536, m = 8192) 52.3 -> 49.5. At 16 KiB they lost: 91.7 -> 99.7 (8192 x 8192 x 1024) and
+// 48.0 -> 51.3 (4096 x 8192 x 1024); at 8 KiB 48.8 -> 51.9 (8192 x 4096 x 1024).
+static bool lds_nt_out(int64_t ldo_bytes) { return ldo_bytes != 8192 && ldo_bytes != 16384; }
+
 static size_t workspace8(const Plan8& p) {
   if (p.splits <= 1) return 0;
   if (p.kind == Kernel8::kStream)  // whole 16x16 tiles of every wave of every column group
@@ -1210,6 +1227,7 @@ int aklr::gemm8_entry(const void* a, int64_t lda, const void* b, int64_t ldb, co
   g.n = (int)n;
   g.k = (int)k;
   g.out_dtype = out_dtype;
+  g.nt_out = lds_nt_out(ldo * 2) ? 1 : 0;
   g.counters = nullptr;
   g.partial = nullptr;
   const bool pre = b_layout == AKLR_B_PRESHUFFLE_16x16;
@@ -1310,6 +1328,7 @@ extern "C" int aklr_quant_gemm_a8w8_blockscale(const void* x, int64_t ldx, const
   g.n = (int)n;
   g.k = (int)k;
   g.out_dtype = out_dtype;
+  g.nt_out = 0;  // the stream kernel's stores are plain
   g.counters = nullptr;
   g.partial = nullptr;
   g.splits = plan.splits;
