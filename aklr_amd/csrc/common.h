@@ -200,6 +200,72 @@ __device__ __forceinline__ uint32_t pack_out2(float a, float b, int out_dtype) {
   return out_dtype == AKLR_OUT_BF16 ? pack_bf16x2(a, b) : (f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16));
 }
 
+// Output tile store through LDS, for a 512-thread workgroup whose LDS operand ring is free. The
+// TM x TN tile is held as 16x16 fp32 accumulators by a WM x WN grid of waves: wave (wm, wn), fragment
+// (mt, nt), lane (li = lane & 15, g = lane >> 4) holds row wm * (TM / WM) + mt * 16 + li, columns
+// wn * (TN / WN) + nt * 16 + 4g .. + 3. Rows [0, TM/2) are packed (bias added) into `lo` and rows
+// [TM/2, TM) into `hi`, as rows of TN * 2 bytes whose 16-byte chunks are XOR-swizzled by row; then
+// each thread moves 16-byte chunks to memory, so that a wave stores 1 KiB of whole tile rows (full
+// 128-byte lines) per instruction, where a lane's own fragments would store two 64-byte halves of
+// each line from two instructions. nt_store selects non-temporal stores. n % 16 == 0.
+template <int TM, int TN, int WM, int WN, int MT, int NT>
+__device__ __forceinline__ void store_tile_via_lds(const f32x4 (&acc)[MT][NT], uint8_t* lo, uint8_t* hi, int wm,
+                                                   int wn, int m0, int n0, int m, int n, void* out, int64_t ldo,
+                                                   const float* bias, int out_dtype, bool nt_store) {
+  constexpr int kCpr = TN / 8;  // 16-byte chunks per tile row
+  constexpr int kSwz = (kCpr & -kCpr) < 8 ? (kCpr & -kCpr) : 8;  // XOR range; divides kCpr
+  constexpr int kHalfRows = TM / 2;
+  static_assert(MT * 16 * WM == TM && NT * 16 * WN == TN && WM % 2 == 0, "wave grid");
+  static_assert(kHalfRows * kCpr % 512 == 0, "whole passes of 512 threads");
+  const int lane = threadIdx.x & 63, li = lane & 15, g = lane >> 4;
+  __syncthreads();  // every wave's last operand reads are done
+  {
+    uint8_t* const half = wm < WM / 2 ? lo : hi;
+    const int r0 = (wm % (WM / 2)) * (TM / WM) + li;  // + mt * 16: the lane's row within its half
+    const int col_w = n0 + wn * (TN / WN) + 4 * g;    // + nt * 16
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      f32x4 bx = {0.f, 0.f, 0.f, 0.f};
+      if (bias) {
+        const int cx = min(col_w + nt * 16, n - 4);  // columns past n are computed, never stored
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bx[r] = bias[cx + r];
+      }
+      const int ch = (wn * (TN / WN) + nt * 16) / 8 + (g >> 1);  // the lane's columns 4g..4g+3
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const f32x4 x = acc[mt][nt] + bx;
+        const u32x2 v = {pack_out2(x[0], x[1], out_dtype), pack_out2(x[2], x[3], out_dtype)};
+        const int r = r0 + mt * 16;
+        *reinterpret_cast<u32x2*>(half + r * (TN * 2) + (ch ^ (r & (kSwz - 1))) * 16 + (g & 1) * 8) = v;
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int kHalfIters = kHalfRows * kCpr / 512;
+  auto store_rows = [&](auto nt_c) {
+#pragma unroll
+    for (int it = 0; it < 2 * kHalfIters; ++it) {
+      const int idx = (it % kHalfIters) * 512 + (int)threadIdx.x;
+      const int r = idx / kCpr, ch = idx % kCpr;
+      const uint8_t* const half = it < kHalfIters ? lo : hi;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(half + r * (TN * 2) + (ch ^ (r & (kSwz - 1))) * 16);
+      const int row = m0 + (it < kHalfIters ? 0 : kHalfRows) + r, col = n0 + ch * 8;
+      if (row < m && col < n) {  // n % 16 == 0: a chunk is wholly inside or past n
+        u32x4* const dst = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(out) + (int64_t)row * ldo + col);
+        if constexpr (decltype(nt_c)::value)
+          __builtin_nontemporal_store(v, dst);
+        else
+          *dst = v;
+      }
+    }
+  };
+  if (nt_store)
+    store_rows(IC<1>{});
+  else
+    store_rows(IC<0>{});
+}
+
 // Split-K partials: layout [split][col][m4] fp32 with m4 = m rounded up to 4, so a lane's 4 rows of
 // one column (an MFMA 16x16 accumulator's rows 4g..4g+3) are one 16-byte access and a wave's
 // accesses are contiguous runs. They travel through device-coherent (sc1) buffer accesses, which go

@@ -35,6 +35,7 @@ struct Gemm4Args {
   int64_t ldo;
   int m, n, k;
   int b_pre, scale_shuffled, out_dtype;
+  int nt_out;   // lds kernel: output stores are non-temporal
   int64_t pc;  // padded scale columns (shuffled layout)
   float* partial;
   uint64_t* counters;  // split-K arrival words, one per output tile (launch-tagged)
@@ -796,8 +797,6 @@ __global__ __launch_bounds__(512) void gemm4_lds_kernel(Gemm4Args p) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  const int row_w = m0 + wm * (TM / 2) + li;
-  const int col_w = n0 + wn * (TN / 4) + 4 * g;
   if (p.splits > 1) {
     // partials in accumulator order, [split][tile][wave][mt][nt][lane] x 4 fp32: the workgroup that
     // reduces them runs the same lanes over the same tiles, so every store and load is 1 KiB of
@@ -825,32 +824,10 @@ __global__ __launch_bounds__(512) void gemm4_lds_kernel(Gemm4Args p) {
     }
   }
 
-  // bf16/fp16 out: lane pairs swap halves so every lane stores 8 consecutive outputs (16 bytes)
-  const int col_s = n0 + wn * (TN / 4) + (g & 1) * 16 + (g >> 1) * 8;
-#pragma unroll
-  for (int nt = 0; nt < NT; nt += 2) {
-    f32x4 bx = {0.f, 0.f, 0.f, 0.f}, by = {0.f, 0.f, 0.f, 0.f};
-    if (p.bias) {
-      const int cx = min(col_w + nt * 16, p.n - 4), cy = min(col_w + nt * 16 + 16, p.n - 4);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        bx[r] = p.bias[cx + r];
-        by[r] = p.bias[cy + r];
-      }
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const f32x4 x = acc[mt][nt] + bx, y = acc[mt][nt + 1] + by;
-      const uint32_t x0 = pack_out2(x[0], x[1], p.out_dtype), x1 = pack_out2(x[2], x[3], p.out_dtype);
-      const uint32_t y0 = pack_out2(y[0], y[1], p.out_dtype), y1 = pack_out2(y[2], y[3], p.out_dtype);
-      const auto s0 = __builtin_amdgcn_permlane16_swap(x0, y0, false, false);
-      const auto s1 = __builtin_amdgcn_permlane16_swap(x1, y1, false, false);
-      const u32x4 v = {s0[0], s1[0], s0[1], s1[1]};
-      const int row = row_w + mt * 16, col = col_s + nt * 16;
-      if (row < p.m && col < p.n)
-        *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + col) = v;
-    }
-  }
+  // Output: whole-line stores through the ring's LDS, rows [0, TM/2) staged in sA and the rest in sB.
+  static_assert((TM / 2) * TN * 2 <= S * kStageA && (TM / 2) * TN * 2 <= S * kStageB, "output staging");
+  store_tile_via_lds<TM, TN, 2, 4, MT, NT>(acc, sA, sB, wm, wn, m0, n0, p.m, p.n, p.out, p.ldo, p.bias, p.out_dtype,
+                                           p.nt_out != 0);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1063,6 +1040,7 @@ extern "C" int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t
   g.b_pre = b_layout == AKLR_B_PRESHUFFLE_16x16;
   g.scale_shuffled = scale_layout == AKLR_SCALES_SHUFFLED;
   g.out_dtype = out_dtype;
+  g.nt_out = ldo * 2 != 8192 && ldo * 2 != 16384;
   g.pc = (k / 32 + 7) / 8 * 8;
   g.partial = nullptr;
   g.counters = nullptr;

@@ -771,7 +771,6 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
     for (int r = 0; r < 4; ++r) acc[tmt(u)][tnt(u)][r] = fmaf(pend[j][r], pend_s[j], acc[tmt(u)][tnt(u)][r]);
   }
 
-  const int col_w = n0 + wn * (TN / WN) + 4 * g;  // + nt * 16: the lane's first output column
   if (p.splits > 1) {
     // partials in accumulator order, [split][tile][wave][mt][nt][lane] x 4 fp32: the workgroup that
     // reduces them runs the same lanes over the same tiles, so every store and load is 1 KiB of
@@ -818,61 +817,10 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
     }
   }
 
-  // Output through LDS, whose ring is free once every wave has left the K loop. Rows [0, TM/2) of the
-  // tile go to sA's bytes and rows [TM/2, TM) to sB's, as rows of TN * 2 bytes whose 16-byte chunks
-  // are XOR-swizzled by row; then each thread moves 16-byte chunks to memory, so that a wave stores
-  // 1 KiB of whole tile rows (full 128-byte lines) per instruction. A lane's own fragments would
-  // store 64 bytes per row, two halves of a line from two instructions.
-  constexpr int kCpr = TN / 8;  // 16-byte chunks per tile row
-  constexpr int kSwz = (kCpr & -kCpr) < 8 ? (kCpr & -kCpr) : 8;  // XOR range; divides kCpr
-  constexpr int kHalfRows = TM / 2;
-  static_assert(kHalfRows * TN * 2 <= S * kStageA && kHalfRows * TN * 2 <= S * kStageB, "output staging");
-  static_assert(kHalfRows * kCpr % 512 == 0 && WM % 2 == 0, "output staging");
-  __syncthreads();  // every wave's last fragment reads are done
-  {
-    uint8_t* const half = wm < WM / 2 ? sA : sB;
-    const int r0 = (wm % (WM / 2)) * (TM / WM) + li;  // + mt * 16: the lane's row within its half
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      f32x4 bx = {0.f, 0.f, 0.f, 0.f};
-      if (p.bias) {
-        const int cx = min(col_w + nt * 16, p.n - 4);  // columns past n are computed, never stored
-#pragma unroll
-        for (int r = 0; r < 4; ++r) bx[r] = p.bias[cx + r];
-      }
-      const int ch = (wn * (TN / WN) + nt * 16) / 8 + (g >> 1);  // the lane's columns 4g..4g+3
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const f32x4 x = acc[mt][nt] + bx;
-        const u32x2 v = {pack_out2(x[0], x[1], p.out_dtype), pack_out2(x[2], x[3], p.out_dtype)};
-        const int r = r0 + mt * 16;
-        *reinterpret_cast<u32x2*>(half + r * (TN * 2) + (ch ^ (r & (kSwz - 1))) * 16 + (g & 1) * 8) = v;
-      }
-    }
-  }
-  __syncthreads();
-  constexpr int kHalfIters = kHalfRows * kCpr / 512;
-  auto store_rows = [&](auto nt_c) {
-#pragma unroll
-    for (int it = 0; it < 2 * kHalfIters; ++it) {
-      const int idx = (it % kHalfIters) * 512 + (int)threadIdx.x;
-      const int r = idx / kCpr, ch = idx % kCpr;
-      const uint8_t* const half = it < kHalfIters ? sA : sB;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(half + r * (TN * 2) + (ch ^ (r & (kSwz - 1))) * 16);
-      const int row = m0 + (it < kHalfIters ? 0 : kHalfRows) + r, col = n0 + ch * 8;
-      if (row < p.m && col < p.n) {  // n % 16 == 0: a chunk is wholly inside or past n
-        u32x4* const dst = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + col);
-        if constexpr (decltype(nt_c)::value)
-          __builtin_nontemporal_store(v, dst);
-        else
-          *dst = v;
-      }
-    }
-  };
-  if (p.nt_out)
-    store_rows(IC<1>{});
-  else
-    store_rows(IC<0>{});
+  // Output: whole-line stores through the ring's LDS, rows [0, TM/2) staged in sA and the rest in sB.
+  static_assert((TM / 2) * TN * 2 <= S * kStageA && (TM / 2) * TN * 2 <= S * kStageB, "output staging");
+  store_tile_via_lds<TM, TN, WM, WN, MT, NT>(acc, sA, sB, wm, wn, m0, n0, p.m, p.n, p.out, p.ldo, p.bias,
+                                             p.out_dtype, p.nt_out != 0);
 }
 
 // ---------------------------------------------------------------------------------------------
