@@ -204,40 +204,68 @@ __device__ __forceinline__ uint32_t pack_out2(float a, float b, int out_dtype) {
 // TM x TN tile is held as 16x16 fp32 accumulators by a WM x WN grid of waves: wave (wm, wn), fragment
 // (mt, nt), lane (li = lane & 15, g = lane >> 4) holds row wm * (TM / WM) + mt * 16 + li, columns
 // wn * (TN / WN) + nt * 16 + 4g .. + 3. Rows [0, TM/2) are packed (bias added) into `lo` and rows
-// [TM/2, TM) into `hi`, as rows of TN * 2 bytes whose 16-byte chunks are XOR-swizzled by row; then
-// each thread moves 16-byte chunks to memory, so that a wave stores 1 KiB of whole tile rows (full
-// 128-byte lines) per instruction, where a lane's own fragments would store two 64-byte halves of
-// each line from two instructions. nt_store selects non-temporal stores. n % 16 == 0.
+// [TM/2, TM) into `hi`, as rows of TN * 2 bytes; then each thread moves 16-byte chunks to memory, so
+// that a wave stores 1 KiB of whole tile rows (full 128-byte lines) per instruction, where a lane's
+// own fragments would store two 64-byte halves of each line from two instructions. nt_store selects
+// non-temporal stores. n % 16 == 0.
+//
+// LDS banks: a 16-byte access serves 8 lanes per 128 bytes of banks. For the writes, permlane16_swap
+// pairs column tiles (nt, nt + 1) so that lane group g holds 8 columns of tile nt + (g & 1); 8 lanes
+// then write one chunk column of 8 consecutive rows. Chunk c of row r sits at c ^ swz(r): with a row
+// pitch of 0 mod 8 chunks (TN = 128, 192, 256) swz(r) = r & 7, with 4 mod 8 (TN = 224: 28 chunks)
+// swz(r) = (r >> 1) & 3, which puts 8 consecutive rows of one chunk column on 8 different 16-byte
+// bank groups, and keeps the 8 chunks a read phase takes from one row on 8 different ones.
 template <int TM, int TN, int WM, int WN, int MT, int NT>
 __device__ __forceinline__ void store_tile_via_lds(const f32x4 (&acc)[MT][NT], uint8_t* lo, uint8_t* hi, int wm,
                                                    int wn, int m0, int n0, int m, int n, void* out, int64_t ldo,
                                                    const float* bias, int out_dtype, bool nt_store) {
   constexpr int kCpr = TN / 8;  // 16-byte chunks per tile row
-  constexpr int kSwz = (kCpr & -kCpr) < 8 ? (kCpr & -kCpr) : 8;  // XOR range; divides kCpr
   constexpr int kHalfRows = TM / 2;
   static_assert(MT * 16 * WM == TM && NT * 16 * WN == TN && WM % 2 == 0, "wave grid");
   static_assert(kHalfRows * kCpr % 512 == 0, "whole passes of 512 threads");
+  static_assert(kCpr % 8 == 0 || kCpr % 8 == 4, "row pitch in chunks");
+  auto at = [](int r, int c) {  // byte offset of chunk c of row r within a half
+    return r * (TN * 2) + (c ^ (kCpr % 8 == 0 ? (r & 7) : ((r >> 1) & 3))) * 16;
+  };
   const int lane = threadIdx.x & 63, li = lane & 15, g = lane >> 4;
   __syncthreads();  // every wave's last operand reads are done
   {
     uint8_t* const half = wm < WM / 2 ? lo : hi;
     const int r0 = (wm % (WM / 2)) * (TM / WM) + li;  // + mt * 16: the lane's row within its half
-    const int col_w = n0 + wn * (TN / WN) + 4 * g;    // + nt * 16
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      f32x4 bx = {0.f, 0.f, 0.f, 0.f};
+    const int c0 = wn * (TN / WN) / 8;               // the wave's first chunk column
+    const int col_w = n0 + wn * (TN / WN) + 4 * g;   // + nt * 16: the lane's first output column
+    auto load_bias = [&](int nt) {
+      f32x4 b = {0.f, 0.f, 0.f, 0.f};
       if (bias) {
         const int cx = min(col_w + nt * 16, n - 4);  // columns past n are computed, never stored
 #pragma unroll
-        for (int r = 0; r < 4; ++r) bx[r] = bias[cx + r];
+        for (int r = 0; r < 4; ++r) b[r] = bias[cx + r];
       }
-      const int ch = (wn * (TN / WN) + nt * 16) / 8 + (g >> 1);  // the lane's columns 4g..4g+3
+      return b;
+    };
+#pragma unroll
+    for (int nt = 0; nt + 1 < NT; nt += 2) {
+      const f32x4 bx = load_bias(nt), by = load_bias(nt + 1);
+      const int c = c0 + (nt + (g & 1)) * 2 + (g >> 1);  // lane group g: 8 columns of tile nt + (g & 1)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const f32x4 x = acc[mt][nt] + bx, y = acc[mt][nt + 1] + by;
+        const uint32_t x0 = pack_out2(x[0], x[1], out_dtype), x1 = pack_out2(x[2], x[3], out_dtype);
+        const uint32_t y0 = pack_out2(y[0], y[1], out_dtype), y1 = pack_out2(y[2], y[3], out_dtype);
+        const auto s0 = __builtin_amdgcn_permlane16_swap(x0, y0, false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(x1, y1, false, false);
+        *reinterpret_cast<u32x4*>(half + at(r0 + mt * 16, c)) = u32x4{s0[0], s1[0], s0[1], s1[1]};
+      }
+    }
+    if constexpr (NT % 2 == 1) {  // the odd last column tile: 8 bytes per lane
+      constexpr int nt = NT - 1;
+      const f32x4 bx = load_bias(nt);
+      const int c = c0 + nt * 2 + (g >> 1);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const f32x4 x = acc[mt][nt] + bx;
         const u32x2 v = {pack_out2(x[0], x[1], out_dtype), pack_out2(x[2], x[3], out_dtype)};
-        const int r = r0 + mt * 16;
-        *reinterpret_cast<u32x2*>(half + r * (TN * 2) + (ch ^ (r & (kSwz - 1))) * 16 + (g & 1) * 8) = v;
+        *reinterpret_cast<u32x2*>(half + at(r0 + mt * 16, c) + (g & 1) * 8) = v;
       }
     }
   }
@@ -249,7 +277,7 @@ __device__ __forceinline__ void store_tile_via_lds(const f32x4 (&acc)[MT][NT], u
       const int idx = (it % kHalfIters) * 512 + (int)threadIdx.x;
       const int r = idx / kCpr, ch = idx % kCpr;
       const uint8_t* const half = it < kHalfIters ? lo : hi;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(half + r * (TN * 2) + (ch ^ (r & (kSwz - 1))) * 16);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(half + at(r, ch));
       const int row = m0 + (it < kHalfIters ? 0 : kHalfRows) + r, col = n0 + ch * 8;
       if (row < m && col < n) {  // n % 16 == 0: a chunk is wholly inside or past n
         u32x4* const dst = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(out) + (int64_t)row * ldo + col);
