@@ -79,9 +79,10 @@ struct XStage {
 // holds one K block per group and the groups' partial sums meet in LDS at the end, in group order, so
 // a narrow workgroup covers its columns over the whole K range with no split-K partials in memory (the
 // plan then runs one K split).
-template <int MT, int NT, int NW, int D, int NS, int FMT, bool PRE, bool QA = false, int KW = 1>
+template <int MT, int NT, int NW, int D, int NS, int FMT, bool PRE, bool QA = false, int KW = 1, bool ROT = false>
 __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p) {
   static_assert(!QA || (MT == 1 && FMT == 0 && NW == 4 && KW == 1), "fused quantization: e4m3, one row tile, 4 waves");
+  static_assert(!ROT || (KW == 1 && !QA), "rotated K order: one K group, no fused quantization");
   static_assert(NS >= 2 && D >= 1 && MT >= 1 && MT <= 8 && 128 % (NT * 16) == 0 && NW % KW == 0, "stream shape");
   constexpr int kSRows = (MT * 16 + 63) / 64 * 64;     // a_scale floats per K block: whole 64-lane loads
   constexpr int kLoadsA = KW * (2 * MT + kSRows / 64);  // loader loads per stage
@@ -90,7 +91,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   // 128-column b_scale blocks under the workgroup: its columns start at a multiple of kCols, so a width
   // that neither divides nor is a multiple of 128 (96, 112) can straddle one more block
   constexpr int kNBlk = kCols % 128 == 0 ? kCols / 128 : (128 % kCols == 0 ? 1 : kCols / 128 + 2);
-  static_assert((NS - 2) * kLoadsA <= 63, "the loader's wait count must fit vmcnt");
+  static_assert((NS - 1) * kLoadsA <= 63, "the loader's wait counts must fit vmcnt");
   __shared__ __attribute__((aligned(1024))) uint8_t sA[NS][KW * MT * 2048];
   __shared__ __attribute__((aligned(16))) float sS[NS][KW * kSRows];
   __shared__ float sSB[kNBlk][512];
@@ -111,6 +112,15 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   const int kb_end = min(KB, kb_begin + p.kb_per_split);
   const int steps = (kb_end - kb_begin + KW - 1) / KW;  // K steps (of KW blocks each)
   const int kw = w / kWC;                               // compute waves: K group
+  // ROT: workgroup x walks its K range from block r0 on, wrapping, so that at any moment the workgroups
+  // fetch different A blocks and weight offsets (r0 spreads evenly over the grid).
+  const int len_k = kb_end - kb_begin;
+  const int r0 = ROT ? (int)((int64_t)blockIdx.x * len_k / gridDim.x) : 0;
+  auto rotk = [&](int kb) {
+    if constexpr (!ROT) return kb;
+    const int t = kb - kb_begin + r0;
+    return kb_begin + (t >= len_k ? t - len_k : t);
+  };
   const int64_t kt32 = p.k >> 5;
 
   f32x4 acc[MT][NT];
@@ -158,8 +168,9 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     auto issue = [&](int t, int st) {  // step t: group j's block t, j < KW
 #pragma unroll
       for (int j = 0; j < KW; ++j) {
-        const int kb = kb_begin + j * steps + t;  // group j's blocks are [kb_begin + j steps, + steps)
-        const bool on = t < steps && kb < kb_end;
+        const int kb0 = kb_begin + j * steps + t;  // group j's blocks are [kb_begin + j steps, + steps)
+        const bool on = t < steps && kb0 < kb_end;
+        const int kb = on ? rotk(kb0) : kb0;
         const uint32_t ak = (uint32_t)kb * 128u, sk = (uint32_t)kb * (uint32_t)(p.sa_sk * 4);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
@@ -179,19 +190,22 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     // stage kb -- fragments are read one K block ahead -- so its slot takes stage kb + NS. Issues past
     // the K range load zeros, which keeps the count exact.
     issue(0, 0);
-    // b_scale of the workgroup's column blocks over its K range (kb_per_split <= 512), staged once,
-    // behind the first A stage; the first stage barrier publishes it with stage 0.
+    // b_scale of the workgroup's column blocks over its K range (kb_per_split <= 512), staged once by
+    // direct-to-LDS loads behind the first A stage and ahead of the others, so stage 0 and b_scale
+    // take one round trip together with every stage in flight; the first stage barrier publishes them.
     {
       const int len = kb_end - kb_begin;
       const int last_row = (p.n - 1) >> 7;
-      for (int i = lane; i < kNBlk * len; i += 64) {
-        const int r = i / len, kk = i - r * len;
-        sSB[r][kk] = p.sb[(int64_t)min((n0 >> 7) + r, last_row) * p.ldbs + kb_begin + kk];
+      const i32x4 sbrs = make_rsrc_words(p.sb, rsrc_bytes(((int64_t)last_row * p.ldbs + KB) * 4));
+      for (int r = 0; r < kNBlk; ++r) {
+        const int64_t row0 = (int64_t)min((n0 >> 7) + r, last_row) * p.ldbs + kb_begin;
+        for (int j0 = 0; j0 < len; j0 += 64)
+          lds_dma4(sbrs, lds_addr(&sSB[r][j0]), j0 + lane < len ? (uint32_t)((row0 + j0 + lane) * 4) : kOobOffset);
       }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage 0 and b_scale have landed
 #pragma unroll
     for (int s = 1; s < NS; ++s) issue(s, s);  // only stage loads from here: the counts are exact
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 1) * kLoadsA) : "memory");  // stage 0 and b_scale
     stage_barrier();
     int st_fill = 0;
     for (int t = 0; t < steps; ++t) {
@@ -217,8 +231,8 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     // Step counter kb runs kb_begin, kb_begin + 1, ...; this wave's K block at step kb is kbw(kb).
     auto kbw = [&](int kb) { return KW == 1 ? kb : kb_begin + kw * steps + (kb - kb_begin); };
     auto load = [&](int kb, StreamFrag<NT>& f) {
-      const int kb_w = kbw(kb);
-      const bool on = kb_w < kb_end && (KW == 1 || kb - kb_begin < steps);
+      const bool on = kbw(kb) < kb_end && (KW == 1 || kb - kb_begin < steps);
+      const int kb_w = on ? rotk(kbw(kb)) : 0;
       const uint32_t boff = on ? (uint32_t)(PRE ? kb_w * 2048 : kb_w * 128) : kOobOffset;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
@@ -334,7 +348,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
       }
       st = st + 1 == NS ? 0 : st + 1;
       // a group's blocks past the K range hold zeros; their b_scale slot was never staged
-      const float sb = KW == 1 ? sbw[kb - kb_begin] : (kbw(kb) < kb_end ? sbw[kbw(kb) - kb_begin] : 0.0f);
+      const float sb = KW == 1 ? sbw[rotk(kb) - kb_begin] : (kbw(kb) < kb_end ? sbw[kbw(kb) - kb_begin] : 0.0f);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const float sc = s[mt] * sb;
@@ -848,6 +862,7 @@ struct Plan8 {
   int tm, tn;        // lds: workgroup tile
   int grid_x;        // stream: column groups; lds: output tiles
   int splits, kb_per_split;
+  bool rot = false;  // stream: the long-K plan (each workgroup walks its K range from its own block)
 };
 
 static void finish_splits(Plan8& p, int64_t KB, int64_t s) {
@@ -995,6 +1010,24 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
       p.nw = best_nw;
       p.nt = best_nt;
       p.grid_x = (int)best_groups;
+      // (one compute wave runs 8 A stages: measured at m = 1 / 16, us, 2112 x 7168 7.11 -> 6.90 / 7.92 -> 7.71)
+    }
+  }
+  // Long K at one row tile (>= 96 K blocks, e.g. 7168 x 16384): one K split, 32-column workgroups of
+  // two compute waves, an 8-deep weight ring behind an 8-stage A ring, and each workgroup starting its
+  // K walk at its own block (r0 = its index x K blocks / workgroups, wrapping), when that makes
+  // 192-256 workgroups. No partials, no split-K epilogue; the spread start keeps the workgroups from
+  // fetching the same A block at once. Measured on cold weights, 7168 x 16384, m = 1 / 16 (us): the
+  // split plan 24.0 / 23.1, this plan 20.8 / 21.9 (21.2 / 22.6 without the rotation; 29.9 / 30.9 with
+  // the 4-stage A ring, whose one round trip per 2-3 K blocks then paces the workgroup).
+  if (fill && p.mt == 1 && p.kw == 1 && KB >= 96) {
+    const int64_t groups = (n + 31) / 32;
+    if (groups >= 192 && groups <= 256) {
+      p.nw = 2;
+      p.nt = 1;
+      p.grid_x = (int)groups;
+      finish_splits(p, KB, 1);
+      p.rot = true;
     }
   }
   // The same at 4 and 8 row tiles, where a workgroup's work is long: 240-256 workgroups (a second
@@ -1047,12 +1080,14 @@ static size_t workspace8(const Plan8& p) {
   return kSplitkCounterBytes + (size_t)p.splits * (size_t)p.grid_x * p.tm * p.tn * sizeof(float);
 }
 
-// Stream kernel: NW compute waves (4 but for the one-row-tile fill plans) and 4 A stages; ring depth 4
-// at 1-2 row tiles, else 2 (measured).
-template <int MT, int NT, int FMT, bool PRE, bool QA = false, int KW = 1, int NW = 4>
+// Stream kernel: NW compute waves (4 but for the fill and long-K plans) and 4 A stages (8 for the
+// one-wave fill plans and the long-K plan); ring depth 4 at 1-2 row tiles, else 2, and 8 for the long-K
+// plan (measured).
+template <int MT, int NT, int FMT, bool PRE, bool QA = false, int KW = 1, int NW = 4, int NS = 4, bool DEEP = false,
+          bool ROT = false>
 static void launch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
-  constexpr int D = MT <= 2 ? 4 : 2;
-  hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, NW, D, 4, FMT, PRE, QA, KW>),
+  constexpr int D = DEEP ? 8 : (MT <= 2 ? 4 : 2);
+  hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, NW, D, NS, FMT, PRE, QA, KW, ROT>),
                      dim3((unsigned)d.grid_x, (unsigned)d.splits), dim3((NW + 1) * 64), 0, s, a);
 }
 
@@ -1061,8 +1096,10 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   if (d.kw > 1) {  // one column tile per wave, 1 or 2 row tiles
     if (d.mt == 1) d.kw == 2 ? launch_stream<1, 1, FMT, PRE, false, 2>(a, d, s) : launch_stream<1, 1, FMT, PRE, false, 4>(a, d, s);
     else d.kw == 2 ? launch_stream<2, 1, FMT, PRE, false, 2>(a, d, s) : launch_stream<2, 1, FMT, PRE, false, 4>(a, d, s);
+  } else if (d.rot) {
+    launch_stream<1, 1, FMT, PRE, false, 1, 2, 8, true, true>(a, d, s);
   } else if (d.mt == 1 && d.nw == 1) {
-    launch_stream<1, 2, FMT, PRE, false, 1, 1>(a, d, s);
+    launch_stream<1, 2, FMT, PRE, false, 1, 1, 8>(a, d, s);
   } else if (d.mt == 1 && d.nw == 3) {
     launch_stream<1, 2, FMT, PRE, false, 1, 3>(a, d, s);
   } else if (d.mt == 1 && d.nw == 7) {
@@ -1086,8 +1123,14 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
 // the workspace and runs the GEMM. Measured on the DeepSeek-V3 shapes: one row tile saves 1-1.5 us a
 // call over the two launches; at 2 row tiles (8 values a lane) the two are even, at 4 (32 values a
 // lane) the quantization outgrows the wait for the weights and the fused call is 15-25% slower.
-static bool fused_quant_ok(const Plan8& p) {
-  return p.kind == Kernel8::kStream && p.mt == 1 && p.kw == 1 && p.nw == 4;
+// The fused kernel runs the 4-wave plan (fill = false); it serves a call only where the GEMM's own plan
+// sums every output in the same order (the same K splits, no rotated K walk), so the fused call equals
+// the two ops bit for bit. Elsewhere the entry point runs the two kernels.
+static bool fused_quant_ok(int64_t m, int64_t n, int64_t k) {
+  const Plan8 f = plan8(m, n, k, false);
+  if (!(f.kind == Kernel8::kStream && f.mt == 1 && f.kw == 1 && f.nw == 4)) return false;
+  const Plan8 t = plan8(m, n, k);
+  return !t.rot && t.splits == f.splits;
 }
 
 template <bool PRE>
@@ -1100,13 +1143,13 @@ static void dispatch_stream_qa(const Gemm8Args& a, const Plan8& d, hipStream_t s
 // codes start past the arrival-word region even when the GEMM runs unsplit, so the region's place is
 // the same in every workspace.
 static size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
-static size_t quant_codes_offset(const Plan8& p) {
-  const size_t gemm = up256(workspace8(p));
+static size_t quant_codes_offset(int64_t m, int64_t n, int64_t k) {  // past the GEMM's own workspace
+  const size_t gemm = up256(workspace8(plan8(m, n, k)));
   return gemm > kSplitkCounterBytes ? gemm : kSplitkCounterBytes;
 }
-static size_t quant_gemm_workspace(const Plan8& p, int64_t m, int64_t k) {
-  if (fused_quant_ok(p)) return workspace8(p);
-  return quant_codes_offset(p) + up256((size_t)m * k) + up256((size_t)(k / 128) * m * 4);
+static size_t quant_gemm_workspace(int64_t m, int64_t n, int64_t k) {
+  if (fused_quant_ok(m, n, k)) return workspace8(plan8(m, n, k, false));
+  return quant_codes_offset(m, n, k) + up256((size_t)m * k) + up256((size_t)(k / 128) * m * 4);
 }
 
 // Ring depth per tile shape: as many stages (at most 4) as 150 KiB of LDS holds.
@@ -1165,6 +1208,8 @@ int aklr::gemm8_entry(const void* a, int64_t lda, const void* b, int64_t ldb, co
   if (((m - 1) * sa_stride_m + (k / 128 - 1) * sa_stride_k + 1) * 4 > 0x7FFFFFFFll) return AKLR_ERR_INVALID_ARGUMENT;
   if (b_layout == AKLR_B_ROW_MAJOR && (ldb < k || ldb % 16 != 0)) return AKLR_ERR_INVALID_ARGUMENT;
   if (ldbs < k / 128 || sa_stride_m < 0 || sa_stride_k < 0) return AKLR_ERR_INVALID_ARGUMENT;
+  // The stream kernel stages b_scale with 32-bit offsets from its start.
+  if (((n - 1) / 128 * ldbs + k / 128) * 4 > 0x7FFFFFFFll) return AKLR_ERR_INVALID_ARGUMENT;
   if (m == 0) return AKLR_OK;
 
   Gemm8Args g;
@@ -1227,12 +1272,12 @@ extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void*
 
 extern "C" size_t aklr_quant_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k < 128) return 0;
-  return quant_gemm_workspace(plan8(m, n, k, false), m, k);
+  return quant_gemm_workspace(m, n, k);
 }
 
 extern "C" int aklr_quant_gemm_a8w8_blockscale_fused(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k < 128) return 0;
-  return fused_quant_ok(plan8(m, n, k, false)) ? 1 : 0;
+  return fused_quant_ok(m, n, k) ? 1 : 0;
 }
 
 extern "C" int aklr_quant_gemm_a8w8_blockscale(const void* x, int64_t ldx, const void* b, int64_t ldb,
@@ -1253,19 +1298,19 @@ extern "C" int aklr_quant_gemm_a8w8_blockscale(const void* x, int64_t ldx, const
   if (ldbs < k / 128) return AKLR_ERR_INVALID_ARGUMENT;
   if (m == 0) return AKLR_OK;
   const Plan8 plan = plan8(m, n, k, false);
-  const size_t need = quant_gemm_workspace(plan, m, k);
+  const size_t need = quant_gemm_workspace(m, n, k);
   if (need > 0 && (!workspace || workspace_bytes < need || !aklr_aligned16(workspace))) return AKLR_ERR_WORKSPACE;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
 
-  if (!fused_quant_ok(plan)) {
+  if (!fused_quant_ok(m, n, k)) {
     // quantize into the workspace (past the GEMM's part), then the GEMM reads it
-    uint8_t* q = ws + quant_codes_offset(plan);
+    uint8_t* q = ws + quant_codes_offset(m, n, k);
     float* sc = reinterpret_cast<float*>(q + up256((size_t)m * k));
     int st = aklr_per_group_quant_fp8(x, ldx, q, sc, m, k, stream);
     if (st != AKLR_OK) return st;
+    const size_t gemm_ws = workspace8(plan8(m, n, k));
     return aklr_gemm_a8w8_blockscale(q, k, b, ldb, sc, 1, m, b_scale, ldbs, bias, out, ldo, m, n, k,
-                                     AKLR_FP8_E4M3FN, b_layout, out_dtype, workspace8(plan) ? ws : nullptr,
-                                     workspace8(plan), stream);
+                                     AKLR_FP8_E4M3FN, b_layout, out_dtype, gemm_ws ? ws : nullptr, gemm_ws, stream);
   }
   // the loader addresses x with 32-bit byte offsets from its first row
   if (((m - 1) * ldx + k) * 2 > 0x7FFFFFFFll) return AKLR_ERR_INVALID_ARGUMENT;

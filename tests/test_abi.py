@@ -83,11 +83,13 @@ def test_workspace_sizes_are_host_computable(native_lib):
 def test_quant_gemm_path_and_workspace_are_host_computable(native_lib):
     L = native_lib
     fused = L.aklr_quant_gemm_a8w8_blockscale_fused
-    # one launch at one row tile on the decode shapes; two kernels past 16 rows, on a wave-split-K plan
-    # (4096 x 8192) and for empty sizes
-    assert fused(16, 7168, 16384) == 1 and fused(1, 2112, 7168) == 1 and fused(4, 24576, 1536) == 1
+    # one launch at one row tile on the decode shapes of up to 56 K blocks; two kernels past 16 rows, on a
+    # wave-split-K plan (4096 x 8192), on the long-K plan (7168 x 16384, whose GEMM walks K in its own
+    # order) and for empty sizes
+    assert fused(16, 2112, 7168) == 1 and fused(1, 2112, 7168) == 1 and fused(4, 24576, 1536) == 1
+    assert fused(16, 4096, 16384) == 1
     assert fused(17, 7168, 16384) == 0 and fused(300, 1024, 2048) == 0
-    assert fused(1, 4096, 8192) == 0
+    assert fused(1, 4096, 8192) == 0 and fused(1, 7168, 16384) == 0 and fused(16, 7168, 16384) == 0
     assert fused(0, 7168, 16384) == 0 and fused(1, 7168, 64) == 0
     # the two-kernel path stages the codes and scales past the 128 KiB arrival-word region
     m, n, k = 20, 2112, 128

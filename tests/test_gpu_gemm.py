@@ -257,6 +257,26 @@ def test_fill_plans(m, n, k, bias, fp16):
     _run_and_check(m, n, k, variant="b_shuffled", seed=62)
 
 
+# The long-K plan (one row tile, >= 96 K blocks, 192-256 workgroups of 32 columns, one K split, each
+# workgroup starting its K walk at its own block): a ragged last workgroup (n = 6160: its second column
+# tile past n) at a K range that 193 workgroups do not divide, 256 workgroups at 100 K blocks, MN scales,
+# bias, fp16 and e5m2. The fused entry runs the two kernels there and equals the two ops bit for bit.
+@pytest.mark.parametrize("m,n,k,mode,bias,fp16,e5", [
+    (13, 6160, 12288, "K", True, True, False),
+    (1, 8192, 12800, "MN", False, False, False),
+    (16, 7168, 16384, "K", False, False, True),
+    (5, 7168, 16384, "MN", True, False, False),
+])
+def test_long_k_plan(m, n, k, mode, bias, fp16, e5):
+    assert aklr_amd._lib.lib().aklr_gemm_a8w8_blockscale_workspace_bytes(m, n, k) == 0, "expected one K split"
+    dtype = torch.float8_e5m2 if e5 else torch.float8_e4m3fn
+    out_dtype = torch.float16 if fp16 else None
+    _run_and_check(m, n, k, mode=mode, bias=bias, out_dtype=out_dtype, dtype=dtype, seed=63, cols=1024)
+    if not e5:
+        _run_and_check(m, n, k, variant="b_shuffled", seed=64, cols=1024)
+        assert aklr_amd._lib.lib().aklr_quant_gemm_a8w8_blockscale_fused(m, n, k) == 0
+
+
 # 192- and 224-column LDS tiles (planned where they divide N): ragged row tiles, bias and fp16 output on
 # the odd last column tile's 8-byte stores, b_scale blocks straddled by a wave's columns (tiles start at
 # multiples of 64 or 32 columns), 256- and 128-row tiles, the 4 x 2 wave layout and the uneven B slabs
@@ -304,11 +324,12 @@ def test_quant_gemm_fused_matches_two_ops(m, n, k, shuffled, bias, fp16):
     info = aklr_amd.quant_gemm_a8w8_blockwise_scaled.serving(x, b if not shuffled else bb, bs, bias=bias_t,
                                                               out_dtype=od,
                                                               operand_format="none:preshuffled" if shuffled else "none:none")
-    # one launch at m <= 16 on the DeepSeek-V3 shapes; elsewhere the library's plan decides (a GEMM plan
-    # that splits K over its waves, e.g. 4096 x 8192 or 4112 x 1024, runs the two kernels)
+    # one launch at m <= 16 on the DeepSeek-V3 shapes of up to 56 K blocks; elsewhere the library's plan
+    # decides (a GEMM plan that splits K over its waves, e.g. 4096 x 8192 or 4112 x 1024, or the long-K
+    # plan of 7168 x 16384, runs the two kernels)
     fused = aklr_amd._lib.lib().aklr_quant_gemm_a8w8_blockscale_fused(m, n, k) == 1
     if m <= 16 and (n, k) in workloads.DEEPSEEK_NK:
-        assert fused
+        assert fused == ((n, k) != (7168, 16384))
     assert info.kernel_ref.endswith(":stream_fused" if fused else (":stream" if m <= 128 else ":lds"))
 
 
