@@ -70,7 +70,7 @@ SIGNATURES: dict[str, tuple] = {
 AKLR_OK = 0
 AKLR_ERR_INVALID_ARGUMENT, AKLR_ERR_UNSUPPORTED, AKLR_ERR_WORKSPACE, AKLR_ERR_LAUNCH = 1, 2, 3, 4
 AKLR_ERR_SCRATCH_LIMIT = 5
-NOALLOC_SCRATCH_BYTES = 32 << 20  # AKLR_NOALLOC_SCRATCH_BYTES
+NOALLOC_SCRATCH_BYTES = 48 << 20  # AKLR_NOALLOC_SCRATCH_BYTES
 FP8_E4M3FN, FP8_E5M2 = 0, 1
 OUT_BF16, OUT_F16 = 0, 1
 B_ROW_MAJOR, B_PRESHUFFLE_16x16 = 0, 1

@@ -222,7 +222,6 @@ __device__ __forceinline__ void store_tile_via_lds(const f32x4 (&acc)[MT][NT], u
   constexpr int kCpr = TN / 8;  // 16-byte chunks per tile row
   constexpr int kHalfRows = TM / 2;
   static_assert(MT * 16 * WM == TM && NT * 16 * WN == TN && WM % 2 == 0, "wave grid");
-  static_assert(kHalfRows * kCpr % 512 == 0, "whole passes of 512 threads");
   static_assert(kCpr % 8 == 0 || kCpr % 8 == 4, "row pitch in chunks");
   auto at = [](int r, int c) {  // byte offset of chunk c of row r within a half
     return r * (TN * 2) + (c ^ (kCpr % 8 == 0 ? (r & 7) : ((r >> 1) & 3))) * 16;
@@ -270,11 +269,14 @@ __device__ __forceinline__ void store_tile_via_lds(const f32x4 (&acc)[MT][NT], u
     }
   }
   __syncthreads();
-  constexpr int kHalfIters = kHalfRows * kCpr / 512;
+  // passes of 512 threads over each half; the last one partial when the half is not a whole number of
+  // them (192-row tiles)
+  constexpr int kHalfChunks = kHalfRows * kCpr, kHalfIters = (kHalfChunks + 511) / 512;
   auto store_rows = [&](auto nt_c) {
 #pragma unroll
     for (int it = 0; it < 2 * kHalfIters; ++it) {
       const int idx = (it % kHalfIters) * 512 + (int)threadIdx.x;
+      if (kHalfChunks % 512 != 0 && idx >= kHalfChunks) continue;
       const int r = idx / kCpr, ch = idx % kCpr;
       const uint8_t* const half = it < kHalfIters ? lo : hi;
       const u32x4 v = *reinterpret_cast<const u32x4*>(half + at(r, ch));

@@ -9,7 +9,8 @@
 //   streams its own weight columns over the workgroup's K range from HBM straight into MFMA operand
 //   registers (a register ring, no LDS), and a loader wave fills an LDS ring with each K block of A
 //   in MFMA fragment order.
-// * lds (m > 128): 256x256, 256x128, 128x256 or 128x128 workgroup tiles of 8 waves, K steps of 128
+// * lds (m > 128): 256x256, 256x224, 256x192, 192x192, 256x128, 128x256, 128x192 or 128x128 workgroup
+//   tiles of 8 waves, K steps of 128
 //   through a 2- to 4-stage LDS ring filled by direct-to-LDS loads (16-byte chunks XOR-swizzled by
 //   row), a_scale staged in LDS, XCD-aware tile order, 16-byte output stores.
 //
@@ -873,9 +874,10 @@ static void finish_splits(Plan8& p, int64_t KB, int64_t s) {
   p.splits = (int)((KB + p.kb_per_split - 1) / p.kb_per_split);
 }
 
-// LDS plan for a given tile and split count. s = 0 picks it: 128x128 and 128x192 tiles split K into
-// as many parts as fill one 512-thread workgroup per CU (at most 4, >= 4 K blocks each); the larger
-// tiles do not split (measured: their partials, 2-4x larger, cost more than the parallelism gains).
+// LDS plan for a given tile and split count. s = 0 picks it: 128x128, 128x192 and 192x192 tiles split K
+// into as many parts as fill one 512-thread workgroup per CU (at most 4, >= 4 K blocks each); the larger
+// tiles do not split (measured: their partials, 2-4x larger, cost more than the parallelism gains;
+// 192x192 at m = 2048 on 2112 x 7168: 2 splits 48.9 us, none 63.0).
 static Plan8 plan8_lds(int64_t m, int64_t n, int64_t k, int tm, int tn, int64_t s = 0) {
   Plan8 p;
   p.kind = Kernel8::kLds;
@@ -887,7 +889,7 @@ static Plan8 plan8_lds(int64_t m, int64_t n, int64_t k, int tm, int tn, int64_t 
   const int64_t tiles = ((m + tm - 1) / tm) * ((n + tn - 1) / tn);
   p.grid_x = (int)tiles;
   if (s <= 0) {
-    s = tiles >= 256 || tm + tn > 320 ? 1 : 256 / tiles;
+    s = tiles >= 256 || (tm + tn > 320 && tm != 192) ? 1 : 256 / tiles;
     if (s > 4) s = 4;
     if (s > KB / 4) s = KB / 4;
   }
@@ -898,14 +900,19 @@ static Plan8 plan8_lds(int64_t m, int64_t n, int64_t k, int tm, int tn, int64_t 
 // Estimated time (us) of an LDS plan, fitted to MI355X measurements over the DeepSeek-V3 shapes at
 // m = 128..8192 (it picks the fastest measured plan, or one within 2% of it, on all of them; and the
 // fastest, or within 4%, of sweeps with the 192- and 224-column tiles at m = 1024..8192): per K block
-// of one tile (256x256: 1.96, 256x224: 1.76, 256x192: 1.55, 256x128 and 128x256: 1.15, 128x192: 0.90,
-// 128x128: 0.70), rounds of 256 workgroups, a fixed 3 us per round, and for a K split the partial
-// traffic (s * tile * 4 bytes, stored and then summed by one workgroup at ~100 GB/s) plus 3 us.
+// of one tile (256x256: 1.96, 256x224: 1.76, 256x192: 1.55, 192x192: 1.25, 256x128 and 128x256: 1.15,
+// 128x192: 0.90, 128x128: 0.70), rounds of 256 workgroups, a fixed 3 us per round, and for a K split the
+// partial traffic (s * tile * 4 bytes, stored and then summed by one workgroup at ~100 GB/s) plus 3 us.
+// The 192x192 tile serves N = 2112 = 11 x 192, where 22 x 11 = 242 tiles fill the chip at m = 4096 and
+// 256-row tiles leave 80 CUs idle (cold operands, us, 256x192 -> 192x192: m = 4096 93.5 -> 72.3,
+// m = 8192 158.0 -> 137.8; 128x192 -> 192x192 at m = 2048: 52.5 -> 48.9). Elsewhere it measured slower
+// than the planned tile on all eleven reference and DeepSeek-V3 prefill shapes tried.
 static double lds_cost(const Plan8& p, int64_t k) {
   const int area = p.tm * p.tn;
   const double step = area == 65536   ? 1.96
                       : area == 57344 ? 1.76
                       : area == 49152 ? 1.55
+                      : area == 36864 ? 1.25
                       : area == 32768 ? 1.15
                       : area == 24576 ? 0.90
                                       : 0.70;
@@ -918,8 +925,8 @@ static double lds_cost(const Plan8& p, int64_t k) {
 }
 
 static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
-  static const int kShapes[7][2] = {{256, 256}, {256, 224}, {256, 192}, {256, 128},
-                                    {128, 256}, {128, 192}, {128, 128}};
+  static const int kShapes[8][2] = {{256, 256}, {256, 224}, {256, 192}, {192, 192},
+                                    {256, 128}, {128, 256}, {128, 192}, {128, 128}};
   Plan8 best = plan8_lds(m, n, k, 128, 128);
   double best_t = lds_cost(best, k);
   for (const auto& sh : kShapes) {
@@ -1163,7 +1170,9 @@ static void launch_lds_t(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
 
 template <int FMT, bool PRE>
 static void launch_lds(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
-  if (t.tm == 256) {
+  if (t.tm == 192) {
+    launch_lds_t<192, 192, FMT, PRE>(a, t, s);
+  } else if (t.tm == 256) {
     if (t.tn == 256) launch_lds_t<256, 256, FMT, PRE>(a, t, s);
     else if (t.tn == 224) launch_lds_t<256, 224, FMT, PRE>(a, t, s);
     else if (t.tn == 192) launch_lds_t<256, 192, FMT, PRE>(a, t, s);

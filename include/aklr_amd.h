@@ -128,7 +128,7 @@ int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void* b, int64_t
  * (it looks the array's address up once per device). Calls on one GPU share the array: calls that may
  * overlap in time (other streams, other host threads) race.
  */
-#define AKLR_NOALLOC_SCRATCH_BYTES (32u << 20)
+#define AKLR_NOALLOC_SCRATCH_BYTES (48u << 20)
 int aklr_gemm_a8w8_blockscale_noalloc(const void* a, int64_t lda, const void* b, int64_t ldb, const float* a_scale,
                                       int64_t sa_stride_m, int64_t sa_stride_k, const float* b_scale, int64_t ldbs,
                                       const float* bias, void* out, int64_t ldo, int64_t m, int64_t n, int64_t k,

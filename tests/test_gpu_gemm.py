@@ -257,6 +257,19 @@ def test_fill_plans(m, n, k, bias, fp16):
     _run_and_check(m, n, k, variant="b_shuffled", seed=62)
 
 
+# The 192x192 LDS tile (planned for N = 2112 = 11 x 192 at m >= 2048): a ragged last row tile (m not a
+# multiple of 192), 2 K splits at m = 2048 (121 tiles), bias and fp16 output on both variants.
+@pytest.mark.parametrize("m,n,k,bias,fp16", [
+    (2048, 2112, 7168, False, False),
+    (4000, 2112, 7168, True, True),
+    (2500, 2112, 1024, True, False),
+])
+def test_192_row_tiles(m, n, k, bias, fp16):
+    out_dtype = torch.float16 if fp16 else None
+    _run_and_check(m, n, k, bias=bias, out_dtype=out_dtype, seed=65, rows=128, cols=512)
+    _run_and_check(m, n, k, variant="b_shuffled", seed=66, rows=128, cols=512)
+
+
 # The long-K plan (one row tile, >= 96 K blocks, 192-256 workgroups of 32 columns, one K split, each
 # workgroup starting its K walk at its own block): a ragged last workgroup (n = 6160: its second column
 # tile past n) at a K range that 193 workgroups do not divide, 256 workgroups at 100 K blocks, MN scales,
