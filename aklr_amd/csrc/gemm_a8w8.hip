@@ -49,9 +49,12 @@ struct Gemm8Args {
 // tiles each and stream those weight columns from HBM straight into a D-deep register ring (loads
 // past the K range use an out-of-range offset: zeros, no memory access); one more wave, the loader,
 // moves each 128-wide K block of A (all MT row tiles) and its a_scale column into an NS-stage LDS ring
-// with direct-to-LDS loads, so A crosses L2 once per workgroup instead of once per wave. A lands in MFMA fragment order -- 1 KiB chunk (mt, h) holds at
-// lane l's 16 bytes row mt * 16 + l % 16, bytes 64h + 16 (l / 16) of the block -- and every compute
-// read is one contiguous ds_read_b128.
+// with direct-to-LDS loads, so A crosses L2 once per workgroup instead of once per wave. A row tile
+// of a stage is 16 rows of 128 bytes, each row fetched whole by 8 lanes of one load (one cache line a
+// row; fragment-order loads took two half lines from two loads), its 16-byte chunks XOR-swizzled by row
+// so that the compute waves' ds_read_b128 of their fragments are free of bank conflicts. (Measured,
+// cold weights, us: m = 128 on 2112 x 7168 16.8 -> 15.4 and on 24576 x 1536 14.7 -> 13.8; m = 16 on
+// 2112 x 7168 7.96 -> 7.56; outputs bitwise the same.)
 // The loader issues only LDS-bound loads and the compute waves only register-bound ones, so both
 // sides' wait counts are exact: the loader waits for its own stage with an immediate count, and the
 // compiler tracks the weight ring. One barrier per K block, fenced for LDS only, hands a stage from
@@ -154,12 +157,16 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     const i32x4 ars = make_rsrc_words(p.a, rsrc_bytes((int64_t)(p.m - 1) * p.lda + p.k));
     const i32x4 sars =
         make_rsrc_words(p.sa, rsrc_bytes(((int64_t)(p.m - 1) * p.sa_sm + (int64_t)(KB - 1) * p.sa_sk + 1) * 4));
-    uint32_t a_off[MT], s_off[kSRows / 64];
+    // Load h of row tile mt moves rows mt * 16 + 8h .. + 7 as whole 128-byte lines: lane l takes chunk
+    // (l % 8) ^ (l / 8) of row 8h + l / 8 into position l % 8 of that row (the layout kLineA describes).
+    uint32_t a_off[MT][2], s_off[kSRows / 64];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int row = mt * 16 + li;
-      a_off[mt] = row < p.m ? (uint32_t)((int64_t)row * p.lda + g * 16) : kOobOffset;
-    }
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int row = mt * 16 + 8 * h + (lane >> 3);
+        a_off[mt][h] = row < p.m ? (uint32_t)((int64_t)row * p.lda + (((lane & 7) ^ (lane >> 3)) << 4)) : kOobOffset;
+      }
 #pragma unroll
     for (int i = 0; i < kSRows / 64; ++i) {
       const int row = i * 64 + lane;
@@ -178,7 +185,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
 #pragma unroll
           for (int h = 0; h < 2; ++h)
             lds_dma16(ars, lds_a0 + st * (KW * MT * 2048) + (j * MT + mt) * 2048 + h * 1024,
-                      on && a_off[mt] != kOobOffset ? a_off[mt] + ak + 64 * h : kOobOffset);
+                      on && a_off[mt][h] != kOobOffset ? a_off[mt][h] + ak : kOobOffset);
 #pragma unroll
         for (int i = 0; i < kSRows / 64; ++i)
           lds_dma4(sars, lds_s0 + (st * KW + j) * (kSRows * 4) + i * 256,
@@ -327,9 +334,15 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     // is refilled with block kb + D.
     i32x8 af[MT];
     float s[MT];
+    // kLineA: a stage's row tile is 16 rows of 128 bytes, chunk c of row r at position c ^ (r & 7) (the
+    // loader's whole-line loads); lane (li, g) reads chunks g and 4 + g of row li, conflict-free. The fused
+    // quantization writes the fragment order instead: lane l's 32 bytes at l * 16 and 1024 + l * 16.
+    constexpr bool kLineA = !QA;
+    const int fa_lo = kLineA ? li * 128 + ((g ^ (li & 7)) << 4) : lane * 16;
+    const int fa_hi = kLineA ? li * 128 + (((4 + g) ^ (li & 7)) << 4) : 1024 + lane * 16;
     auto read_frags = [&](int mt, int slot) {
-      af[mt] = cat(*reinterpret_cast<const u32x4*>(&sA[slot][(kw * MT + mt) * 2048 + lane * 16]),
-                   *reinterpret_cast<const u32x4*>(&sA[slot][(kw * MT + mt) * 2048 + 1024 + lane * 16]));
+      af[mt] = cat(*reinterpret_cast<const u32x4*>(&sA[slot][(kw * MT + mt) * 2048 + fa_lo]),
+                   *reinterpret_cast<const u32x4*>(&sA[slot][(kw * MT + mt) * 2048 + fa_hi]));
       s[mt] = sS[slot][kw * kSRows + mt * 16 + li];
     };
     stage_barrier();  // publishes stage kb_begin
