@@ -245,9 +245,10 @@ __global__ __launch_bounds__(NW * 64) void gemm4_skinny_kernel(Gemm4Args p) {
 // stream (16 < m <= 32): the FP8 stream kernel's design (gemm_a8w8.hip) on e2m1. A workgroup owns
 // NW * NT * 16 output columns and a K range of 256-value blocks (128 bytes of codes per row). Its NW
 // compute waves stream their NT weight tiles from HBM straight into a D-deep register ring (codes and
-// the tiles' e8m0 scales); one loader wave moves each K block of A -- the codes in MFMA fragment order
-// (1 KiB chunk (mt, h): lane l's 16 bytes are row mt * 16 + l % 16, bytes 64h + 16 (l / 16) of the
-// block) and the rows' 8 scale bytes, 256 bytes per 32 rows in the caller's layout -- into an
+// the tiles' e8m0 scales); one loader wave moves each K block of A -- the codes as whole 128-byte rows
+// (row r of row tile mt at mt * 2048 + r * 128, its 16-byte chunk c at position c ^ (r & 7), so the
+// fragment reads are conflict-free) and the rows' 8 scale bytes, 256 bytes per 32 rows in the
+// caller's layout -- into an
 // NS-stage LDS ring. One LDS-fenced barrier per block hands a stage over; the MFMA applies both
 // scales, so there is no fold. Lane groups past k load zero codes and take scale 1.0, so padding scale
 // bytes never reach the MFMA. Row-major scales need 4-byte-aligned rows (stream4_ok).
@@ -300,12 +301,17 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm4_stream_kernel(Gemm4Args p
     const i32x4 ars = make_rsrc_words(p.a, rsrc_bytes((int64_t)(p.m - 1) * p.lda + kbytes));
     const i32x4 sars = SSHUF ? make_rsrc_words(p.sa, rsrc_bytes((int64_t)p.pr_a * p.pc))
                              : make_rsrc_words(p.sa, rsrc_bytes((int64_t)(p.m - 1) * p.lds_a + kcols));
-    uint32_t a_off[MT], s_off[kSGroups];
+    // Load h of row tile mt moves rows mt * 16 + 8h .. + 7 as whole 128-byte lines: lane l takes chunk
+    // cl = (l % 8) ^ (l / 8) of row 8h + l / 8 into position l % 8 of that row (chunks XOR-swizzled by row).
+    const int cl = (lane & 7) ^ (lane >> 3);
+    uint32_t a_off[MT][2], s_off[kSGroups];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int row = mt * 16 + li;
-      a_off[mt] = row < p.m ? (uint32_t)((int64_t)row * p.lda + g * 16) : kOobOffset;
-    }
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int row = mt * 16 + 8 * h + (lane >> 3);
+        a_off[mt][h] = row < p.m ? (uint32_t)((int64_t)row * p.lda + cl * 16) : kOobOffset;
+      }
 #pragma unroll
     for (int r = 0; r < kSGroups; ++r) {
       if (SSHUF) {
@@ -322,9 +328,9 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm4_stream_kernel(Gemm4Args p
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const int64_t byte = (int64_t)kb * 128 + 64 * h + g * 16;  // this lane's granule along the row
+          const int64_t byte = (int64_t)kb * 128 + cl * 16;  // this lane's granule along the row
           lds_dma16(ars, lds_a0 + st * (MT * 2048) + mt * 2048 + h * 1024,
-                    on && byte < kbytes && a_off[mt] != kOobOffset ? a_off[mt] + (uint32_t)(kb * 128 + 64 * h) : kOobOffset);
+                    on && byte < kbytes && a_off[mt][h] != kOobOffset ? a_off[mt][h] + (uint32_t)(kb * 128) : kOobOffset);
         }
 #pragma unroll
       for (int r = 0; r < kSGroups; ++r)
@@ -397,7 +403,8 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm4_stream_kernel(Gemm4Args p
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) af[mt][h] = fp4_frag(*reinterpret_cast<const u32x4*>(A + mt * 2048 + h * 1024 + lane * 16));
+        for (int h = 0; h < 2; ++h)  // K step h: chunk 4h + g of row li
+          af[mt][h] = fp4_frag(*reinterpret_cast<const u32x4*>(A + mt * 2048 + li * 128 + (((4 * h + g) ^ (li & 7)) << 4)));
         const int row = mt * 16 + li;
         if (SSHUF) {
           sw[mt] = *reinterpret_cast<const uint32_t*>(S + (row >> 5) * 256 + (g * 16 + (row & 15)) * 4);
