@@ -481,7 +481,7 @@ def decode_floor_figures(dev, stream, weights=None, steps=20):
 
 def probe_prefill(dev, stream, calls=6):
     """The program the prefill counters are read on: the FP8 prefill GEMM at M=4096 on the three
-    DeepSeek-V3 shapes (the 256x192, 256x224 and 256x256 LDS plans), each called ``calls`` times on
+    DeepSeek-V3 shapes (the 192x192, 256x256 and 256x224 LDS plans), each called ``calls`` times on
     rotating cold operand copies, after one warm-up call per copy."""
     import aklr_amd
     from aklr_amd import layouts, workloads
