@@ -877,6 +877,7 @@ struct Plan8 {
   int grid_x;        // stream: column groups; lds: output tiles
   int splits, kb_per_split;
   bool rot = false;  // stream: the long-K plan (each workgroup walks its K range from its own block)
+  int dd = 0;        // stream: weight-ring depth when not the default (4 at 1-2 row tiles, 2 beyond)
 };
 
 static void finish_splits(Plan8& p, int64_t KB, int64_t s) {
@@ -1075,6 +1076,10 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
       p.grid_x = (int)best_groups;
     }
   }
+  // Long K at 7 waves of 4 or 8 row tiles: a deeper weight ring, 4 or 3 blocks (measured on cold weights,
+  // 7168 x 16384, medians of interleaved runs, us: m = 64 26.26 -> 25.94, m = 128 33.50 -> 33.26; on
+  // K <= 56 blocks the deeper rings were even or slower).
+  if (fill && (p.mt == 4 || p.mt == 8) && p.nw == 7 && KB >= 96) p.dd = p.mt == 4 ? 4 : 3;
   return p;
 }
 
@@ -1102,11 +1107,11 @@ static size_t workspace8(const Plan8& p) {
 
 // Stream kernel: NW compute waves (4 but for the fill and long-K plans) and 4 A stages (8 for the
 // one-wave fill plans and the long-K plan); ring depth 4 at 1-2 row tiles, else 2, and 8 for the long-K
-// plan (measured).
-template <int MT, int NT, int FMT, bool PRE, bool QA = false, int KW = 1, int NW = 4, int NS = 4, bool DEEP = false,
+// plan, 4 and 3 for 7-wave plans of 4 and 8 row tiles at >= 96 K blocks (measured).
+template <int MT, int NT, int FMT, bool PRE, bool QA = false, int KW = 1, int NW = 4, int NS = 4, int DD = 0,
           bool ROT = false>
 static void launch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
-  constexpr int D = DEEP ? 8 : (MT <= 2 ? 4 : 2);
+  constexpr int D = DD ? DD : (MT <= 2 ? 4 : 2);
   hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, NW, D, NS, FMT, PRE, QA, KW, ROT>),
                      dim3((unsigned)d.grid_x, (unsigned)d.splits), dim3((NW + 1) * 64), 0, s, a);
 }
@@ -1117,7 +1122,7 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
     if (d.mt == 1) d.kw == 2 ? launch_stream<1, 1, FMT, PRE, false, 2>(a, d, s) : launch_stream<1, 1, FMT, PRE, false, 4>(a, d, s);
     else d.kw == 2 ? launch_stream<2, 1, FMT, PRE, false, 2>(a, d, s) : launch_stream<2, 1, FMT, PRE, false, 4>(a, d, s);
   } else if (d.rot) {
-    launch_stream<1, 1, FMT, PRE, false, 1, 2, 8, true, true>(a, d, s);
+    launch_stream<1, 1, FMT, PRE, false, 1, 2, 8, 8, true>(a, d, s);
   } else if (d.mt == 1 && d.nw == 1) {
     launch_stream<1, 2, FMT, PRE, false, 1, 1, 8>(a, d, s);
   } else if (d.mt == 1 && d.nw == 3) {
@@ -1129,12 +1134,12 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   else if (d.mt == 4) {
     if (d.nw == 2) launch_stream<4, 1, FMT, PRE, false, 1, 2>(a, d, s);
     else if (d.nw == 6) launch_stream<4, 1, FMT, PRE, false, 1, 6>(a, d, s);
-    else if (d.nw == 7) launch_stream<4, 1, FMT, PRE, false, 1, 7>(a, d, s);
+    else if (d.nw == 7) d.dd ? launch_stream<4, 1, FMT, PRE, false, 1, 7, 4, 4>(a, d, s) : launch_stream<4, 1, FMT, PRE, false, 1, 7>(a, d, s);
     else d.nt == 2 ? launch_stream<4, 2, FMT, PRE>(a, d, s) : launch_stream<4, 1, FMT, PRE>(a, d, s);
   } else {
     if (d.nw == 2) launch_stream<8, 1, FMT, PRE, false, 1, 2>(a, d, s);
     else if (d.nw == 6) launch_stream<8, 1, FMT, PRE, false, 1, 6>(a, d, s);
-    else if (d.nw == 7) launch_stream<8, 1, FMT, PRE, false, 1, 7>(a, d, s);
+    else if (d.nw == 7) d.dd ? launch_stream<8, 1, FMT, PRE, false, 1, 7, 4, 3>(a, d, s) : launch_stream<8, 1, FMT, PRE, false, 1, 7>(a, d, s);
     else d.nt == 2 ? launch_stream<8, 2, FMT, PRE>(a, d, s) : launch_stream<8, 1, FMT, PRE>(a, d, s);
   }
 }
