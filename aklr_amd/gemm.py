@@ -236,7 +236,8 @@ def quant_gemm_a8w8_blockwise_scaled(x, b, b_scale, bias=None, out_dtype=None, o
     bit: bf16 activations x [m, k] are quantized per 1 x 128 group (aklr/ops/quant/reference.py:9-28) and
     multiplied by the 128 x 128-block-scaled e4m3 weight (aklr/ops/gemm/reference.py:90-105). This is the
     pair of ops sglang's fp8 block-quant linear calls; for m <= 16 the GEMM's compute waves quantize each K
-    block themselves (one launch, no codes or scales in HBM). b: e4m3fn [n, k] ("none:none") or aiter's 16x16
+    block themselves (one launch, no codes or scales in HBM) wherever the GEMM's own plan sums in the same
+    order (not on wave-split-K or long-K plans, which run the two kernels). b: e4m3fn [n, k] ("none:none") or aiter's 16x16
     preshuffled layout ("none:preshuffled"); b_scale fp32 [ceil(n/128), k/128]; bias fp32 [n] or None.
     Calls it does not serve return a ``FallbackReason``."""
     if not all(isinstance(t, torch.Tensor) for t in (x, b, b_scale)) or (bias is not None and not isinstance(bias, torch.Tensor)):

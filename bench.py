@@ -161,7 +161,8 @@ def build_decode(dev, shuffled=True):
 
 def fused_step_fn(weights, xs, shuffled):
     """The decode step through quant_gemm_a8w8_blockwise_scaled: the same 15 quantize-then-GEMM pairs,
-    one call each (one launch at M <= 16, where the GEMM quantizes its own activations)."""
+    one call each (one launch at M <= 16 where the GEMM quantizes its own activations: 2112x7168 and
+    24576x1536; 7168x16384's long-K plan runs the two kernels)."""
     import aklr_amd
     from aklr_amd import workloads
 
