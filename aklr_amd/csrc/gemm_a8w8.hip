@@ -8,7 +8,7 @@
 // * stream (m <= 128): weight streaming with the activations shared through LDS. Each compute wave
 //   streams its own weight columns over the workgroup's K range from HBM straight into MFMA operand
 //   registers (a register ring, no LDS), and a loader wave fills an LDS ring with each K block of A
-//   in MFMA fragment order.
+//   (whole 128-byte rows, chunks XOR-swizzled by row).
 // * lds (m > 128): 256x256, 256x224, 256x192, 192x192, 256x128, 128x256, 128x192 or 128x128 workgroup
 //   tiles of 8 waves, K steps of 128
 //   through a 2- to 4-stage LDS ring filled by direct-to-LDS loads (16-byte chunks XOR-swizzled by
@@ -52,9 +52,9 @@ struct Gemm8Args {
 // with direct-to-LDS loads, so A crosses L2 once per workgroup instead of once per wave. A row tile
 // of a stage is 16 rows of 128 bytes, each row fetched whole by 8 lanes of one load (one cache line a
 // row; fragment-order loads took two half lines from two loads), its 16-byte chunks XOR-swizzled by row
-// so that the compute waves' ds_read_b128 of their fragments are free of bank conflicts. (Measured,
-// cold weights, us: m = 128 on 2112 x 7168 16.8 -> 15.4 and on 24576 x 1536 14.7 -> 13.8; m = 16 on
-// 2112 x 7168 7.96 -> 7.56; outputs bitwise the same.)
+// so that the compute waves' ds_read_b128 of their fragments are free of bank conflicts. (Measured in
+// single runs on cold weights, us: m = 128 on 2112 x 7168 16.8 -> 15.4 and on 24576 x 1536 14.7 -> 13.8;
+// m = 16 on 2112 x 7168 7.96 -> 7.56; outputs bitwise the same.)
 // The loader issues only LDS-bound loads and the compute waves only register-bound ones, so both
 // sides' wait counts are exact: the loader waits for its own stage with an immediate count, and the
 // compiler tracks the weight ring. One barrier per K block, fenced for LDS only, hands a stage from
@@ -919,8 +919,8 @@ static Plan8 plan8_lds(int64_t m, int64_t n, int64_t k, int tm, int tn, int64_t 
 // partial traffic (s * tile * 4 bytes, stored and then summed by one workgroup at ~100 GB/s) plus 3 us.
 // The 192x192 tile serves N = 2112 = 11 x 192, where 22 x 11 = 242 tiles fill the chip at m = 4096 and
 // 256-row tiles leave 80 CUs idle (cold operands, us, 256x192 -> 192x192: m = 4096 93.5 -> 72.3,
-// m = 8192 158.0 -> 137.8; 128x192 -> 192x192 at m = 2048: 52.5 -> 48.9). Elsewhere it measured slower
-// than the planned tile on all eleven reference and DeepSeek-V3 prefill shapes tried.
+// m = 8192 158.0 -> 137.8; 128x192 -> 192x192 at m = 2048: 52.5 -> 48.9). On ten other reference and
+// DeepSeek-V3 prefill shapes it measured slower than the planned tile or within 2% of it.
 static double lds_cost(const Plan8& p, int64_t k) {
   const int area = p.tm * p.tn;
   const double step = area == 65536   ? 1.96
