@@ -1031,7 +1031,8 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
       p.nw = best_nw;
       p.nt = best_nt;
       p.grid_x = (int)best_groups;
-      // (one compute wave runs 8 A stages: measured at m = 1 / 16, us, 2112 x 7168 7.11 -> 6.90 / 7.92 -> 7.71)
+      // (one compute wave runs 8 A stages; with the loader's overlapped prologue, measured against the 4-stage
+      // kernel before it at m = 1 / 16, us, 2112 x 7168: 7.11 -> 6.90 / 7.92 -> 7.71)
     }
   }
   // Long K at one row tile (>= 96 K blocks, e.g. 7168 x 16384): one K split, 32-column workgroups of
