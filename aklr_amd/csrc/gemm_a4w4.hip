@@ -878,9 +878,9 @@ static void launch_skinny4(const Gemm4Args& g, const Skinny4Plan& p, hipStream_t
 
 // Stream plan for 16 < m <= 32 (two row tiles; measured on MI355X over the Llama-70B MXFP4 shapes,
 // where the stream kernel beats the skinny kernel by 18-20% at m = 32 but not at m = 1, and the LDS
-// kernel from m = 64): 4 compute waves of one column tile each, or 8 waves of two once n >= 32768;
-// ring depth 2; K split in 2 or 4 (a power of two) until about 2048 compute waves run. Row-major
-// scales need 4-byte-aligned rows (direct-to-LDS loads of whole dwords).
+// kernel from m = 64): 4 compute waves of one column tile each (8 A stages), or 8 waves of two once
+// n >= 32768 (4 A stages); ring depth 2; K split in 2 or 4 (a power of two) until about 2048 compute
+// waves run. Row-major scales need 4-byte-aligned rows (direct-to-LDS loads of whole dwords).
 static constexpr int64_t kStream4MinM = 17;
 
 struct Stream4Plan {
@@ -915,8 +915,8 @@ static void launch_stream4(const Gemm4Args& g, const Stream4Plan& p, hipStream_t
   const dim3 grid((unsigned)p.groups, (unsigned)p.splits);
   if (p.nt == 2)
     hipLaunchKernelGGL((gemm4_stream_kernel<2, 2, 8, 2, 4, PRE, SSHUF>), grid, dim3(9 * 64), 0, s, g);
-  else
-    hipLaunchKernelGGL((gemm4_stream_kernel<2, 1, 4, 2, 4, PRE, SSHUF>), grid, dim3(5 * 64), 0, s, g);
+  else  // 8 A stages (interleaved medians, m = 32, us: 10240 x 8192 14.29 -> 13.98, 8192 x 28672 26.27 -> 26.17)
+    hipLaunchKernelGGL((gemm4_stream_kernel<2, 1, 4, 2, 8, PRE, SSHUF>), grid, dim3(5 * 64), 0, s, g);
 }
 
 // LDS-kernel plan for m > 32 when k % 256 == 0 (and, for row-major scales, 4-byte aligned scale rows):
