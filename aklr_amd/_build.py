@@ -19,7 +19,8 @@ BUILD_DIR = PKG / "_build"
 LIB_PATH = PKG / "libaklr_amd.so"
 ARCH = "gfx950"
 
-# Packed-fp32 VALU ops are switched off: the kernels' fp32 arithmetic stays scalar per lane.
+# Packed-fp32 VALU ops are switched off: the kernels' fp32 arithmetic stays scalar per lane. The sources
+# also switch them off themselves (AKLR_SCALAR_FP32_BEGIN/END), for builds that pass no such flag.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",

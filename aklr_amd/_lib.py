@@ -35,6 +35,7 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_int, _c_int, _c_int, _vp],
     ),
+    "aklr_noalloc_scratch": (_c_int, [ctypes.POINTER(_vp), ctypes.POINTER(_c_size)]),
     "aklr_transpose_b8": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp]),
     "aklr_quant_gemm_a8w8_blockscale_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "aklr_quant_gemm_a8w8_blockscale_fused": (_c_int, [_c_i64, _c_i64, _c_i64]),

@@ -8,6 +8,22 @@
 
 #include "../../include/aklr_amd.h"
 
+// Packed fp32 VALU instructions (v_pk_fma_f32, v_pk_mul_f32, v_pk_add_f32) are switched off for all
+// device code of this library, in the source, so that every build of these files -- this library's
+// own, and an AKLR schema package built with AKLR's plain -O3 -- keeps the fp32 arithmetic scalar per
+// lane. Each kernel source opens AKLR_SCALAR_FP32_BEGIN after its includes and closes
+// AKLR_SCALAR_FP32_END at its end (a clang attribute push must be popped in the same file).
+#if defined(__HIP_DEVICE_COMPILE__)
+#define AKLR_SCALAR_FP32_BEGIN \
+  _Pragma("clang attribute push (__attribute__((target(\"no-packed-fp32-ops\"))), apply_to = function)")
+#define AKLR_SCALAR_FP32_END _Pragma("clang attribute pop")
+#else
+#define AKLR_SCALAR_FP32_BEGIN
+#define AKLR_SCALAR_FP32_END
+#endif
+
+AKLR_SCALAR_FP32_BEGIN
+
 namespace aklr {
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
@@ -316,14 +332,19 @@ __host__ __device__ inline int64_t round4(int64_t m) { return (m + 3) / 4 * 4; }
 // Split-K arrival words. One 64-bit word per output tile: bits 63..8 hold a tag of the launch, bits
 // 7..0 how many of the launch's workgroups of that tile have arrived. The tag is the dispatch packet's
 // id (its index in the HSA queue, new for every launch, graph replays included) xor a hash of the
-// queue's address (ids of two queues count from the same start), so a word whose tag is not this
-// launch's is a leftover of an earlier call, or garbage, and counts as zero arrivals. No call depends
-// on what the workspace held before it; calls that may run at the same time need their own workspace.
+// queue's address (ids of two queues count from the same start), with bit 63 set, so a word whose tag
+// is not this launch's is a leftover of an earlier call, or garbage, and counts as zero arrivals. The
+// workgroup that completes a tile's count writes the reserved word kWordIdle (0: bit 63 clear, so no
+// launch's tag), so a word that a finished launch used never holds a tag that a later launch could
+// produce again (a queue made again at the same address restarts its dispatch ids); only words of a
+// launch that did not finish, or never-used memory, rely on the tag. No call depends on what the
+// workspace held before it; calls that may run at the same time need their own workspace.
 extern "C" __device__ uint64_t aklr_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
 constexpr uint64_t kTagMask = ~(uint64_t)0xFF;
+constexpr uint64_t kWordIdle = 0;
 __device__ __forceinline__ uint64_t launch_tag() {
   const uint64_t q = (uint64_t)(uintptr_t)__builtin_amdgcn_queue_ptr();
-  return (aklr_dispatch_id() ^ ((q * 0x9E3779B97F4A7C15ull) >> 8)) << 8;
+  return ((aklr_dispatch_id() ^ ((q * 0x9E3779B97F4A7C15ull) >> 8)) << 8) | (1ull << 63);
 }
 
 // The tile's word as the kernel starts, read by the thread that will arrive for its workgroup (before
@@ -340,9 +361,10 @@ __device__ __forceinline__ uint64_t splitk_peek(const uint64_t* word) {
 // when another workgroup of the launch got there first -- in flight together with the partial
 // stores; once those are acknowledged it adds one arrival, and the workgroup that brings the count
 // to `splits` returns true. That one owns the reduction, which it reads with load_partial4 and sums
-// in split order, so the result does not depend on the arrival order. Nothing is reset: the next
-// launch's tag differs. `seen` is splitk_peek's value (meaningful in the arriver only); `slot` is
-// the workgroup's LDS word for the broadcast.
+// in split order, so the result does not depend on the arrival order. The arrival that completes the
+// count stores kWordIdle (no workgroup of the launch touches the word after it). `seen` is
+// splitk_peek's value (meaningful in the arriver only); `slot` is the workgroup's LDS word for the
+// broadcast.
 __device__ __forceinline__ bool splitk_arrive(uint64_t* word, uint64_t seen, int splits, unsigned* slot,
                                               unsigned arriver = 0) {
   const uint64_t tag = launch_tag();
@@ -363,6 +385,8 @@ __device__ __forceinline__ bool splitk_arrive(uint64_t* word, uint64_t seen, int
                                                      __HIP_MEMORY_SCOPE_AGENT);
     const uint64_t old = __hip_atomic_fetch_add(word, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *slot = (unsigned)(old & 0xFF);
+    if ((old & 0xFF) == (uint64_t)(splits - 1))
+      __hip_atomic_store(word, kWordIdle, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   return *slot == (unsigned)(splits - 1);
@@ -385,6 +409,8 @@ int gemm8_entry(const void* a, int64_t lda, const void* b, int64_t ldb, const fl
                 size_t workspace_bytes, void* scratch, size_t scratch_cap, hipStream_t stream);
 
 }  // namespace aklr
+
+AKLR_SCALAR_FP32_END
 
 #define AKLR_LAUNCH_CHECK()                          \
   do {                                               \

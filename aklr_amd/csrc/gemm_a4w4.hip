@@ -19,6 +19,8 @@
 // K % 64 == 0: a K step reaching past K reads zero codes and unit scales there.
 #include "common.h"
 
+AKLR_SCALAR_FP32_BEGIN
+
 namespace aklr {
 
 struct Gemm4Args {
@@ -1109,3 +1111,5 @@ extern "C" int aklr_gemm_a4w4_mxfp4(const uint8_t* a, int64_t lda, const uint8_t
   AKLR_LAUNCH_CHECK();
   return AKLR_OK;
 }
+
+AKLR_SCALAR_FP32_END

@@ -20,6 +20,8 @@
 // launch, and every sum has a fixed order, so results are bitwise reproducible.
 #include "common.h"
 
+AKLR_SCALAR_FP32_BEGIN
+
 namespace aklr {
 
 struct Gemm8Args {
@@ -831,7 +833,10 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
       }
     // Splits go in batches of up to kBatch whose loads are all issued before any is added (each
     // coherent load costs a trip to the memory side); slots past the last split load zeros.
-    constexpr int kBatch = MT * NT <= 8 ? 4 : 1;  // only 128x128 tiles split K (plan8_lds)
+    // The split tiles are 128x128 (MT * NT = 8: 4 splits in flight, 128 VGPRs of loads), 128x192 and
+    // 192x192 (12 and 18: one split at a time; a batch of 2 would hold 96 or 144 more VGPRs beside the
+    // accumulators, past the 256 a wave of this 512-thread kernel has).
+    constexpr int kBatch = MT * NT <= 8 ? 4 : 1;
     for (int sp0 = 0; sp0 < p.splits; sp0 += kBatch) {
       f32x4 v[kBatch][MT][NT];
 #pragma unroll
@@ -1423,3 +1428,5 @@ extern "C" int aklr_transpose_b8(const void* src, int64_t rows, int64_t cols, in
   AKLR_LAUNCH_CHECK();
   return AKLR_OK;
 }
+
+AKLR_SCALAR_FP32_END

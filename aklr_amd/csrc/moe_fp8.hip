@@ -19,6 +19,8 @@
 // count from device memory, so the whole pipeline runs without a host synchronization.
 #include "common.h"
 
+AKLR_SCALAR_FP32_BEGIN
+
 namespace aklr {
 namespace moe {
 
@@ -907,3 +909,5 @@ extern "C" int aklr_deepseek_v2_fp8_moe(const void* hidden, const void* router_w
                      static_cast<const uint8_t*>(w1), w1_scale, static_cast<const uint8_t*>(w2), w2_scale, w_layout,
                      static_cast<uint16_t*>(out), ws, L, stream);
 }
+
+AKLR_SCALAR_FP32_END

@@ -13,6 +13,8 @@
 
 #include <mutex>
 
+AKLR_SCALAR_FP32_BEGIN
+
 namespace aklr {
 
 static __device__ __align__(256) uint8_t scratch[AKLR_NOALLOC_SCRATCH_BYTES];
@@ -48,3 +50,12 @@ extern "C" int aklr_gemm_a8w8_blockscale_noalloc(const void* a, int64_t lda, con
   return aklr::gemm8_entry(a, lda, b, ldb, a_scale, sa_stride_m, sa_stride_k, b_scale, ldbs, bias, out, ldo, m, n,
                            k, fp8_dtype, b_layout, out_dtype, nullptr, 0, ptr, AKLR_NOALLOC_SCRATCH_BYTES, stream);
 }
+
+extern "C" int aklr_noalloc_scratch(void** ptr, size_t* bytes) {
+  if (!ptr || !bytes) return AKLR_ERR_INVALID_ARGUMENT;
+  const int st = aklr::scratch_on_current_device(ptr);
+  *bytes = st == AKLR_OK ? (size_t)AKLR_NOALLOC_SCRATCH_BYTES : 0;
+  return st;
+}
+
+AKLR_SCALAR_FP32_END

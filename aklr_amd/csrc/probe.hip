@@ -5,6 +5,8 @@
 // compared against a constant, so nothing is written unless the data happen to match it.
 #include "common.h"
 
+AKLR_SCALAR_FP32_BEGIN
+
 namespace aklr {
 
 template <int U>
@@ -41,3 +43,5 @@ extern "C" int aklr_probe_hbm_read(const void* src, int64_t bytes, uint32_t* sin
   AKLR_LAUNCH_CHECK();
   return AKLR_OK;
 }
+
+AKLR_SCALAR_FP32_END

@@ -4,6 +4,8 @@
 // lanes that share a group, codes and scales written once.
 #include "common.h"
 
+AKLR_SCALAR_FP32_BEGIN
+
 namespace aklr {
 
 // ---------------------------------------------------------------------------------------------
@@ -312,3 +314,5 @@ extern "C" int aklr_dynamic_mxfp4_quant(const void* x, int64_t x_row_stride, uin
   AKLR_LAUNCH_CHECK();
   return AKLR_OK;
 }
+
+AKLR_SCALAR_FP32_END

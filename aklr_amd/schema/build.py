@@ -2,9 +2,10 @@
 aklr/core/runtime/builder/builder.py:256-298): the sources written out at their paths,
 ``torch.utils.cpp_extension.load`` of the ``.hip`` files with the source root on the include path,
 ``-O3`` for the arch alone, the extension (and op namespace) named ``aklr_hip_<16 hex digits of the
-content hash>``, loaded with ``torch.ops.load_library``. One flag is added: packed fp32 VALU ops off, as
-for the rest of this library. The libraries go in-tree under ``aklr_amd/schema/_built/`` so that a GPU
-run loads what was built here, and ``op_schema_errors`` restates the builder's check of the op it
+content hash>``, loaded with ``torch.ops.load_library``. No flag is added: the sources themselves switch
+packed fp32 VALU ops off (AKLR_SCALAR_FP32_BEGIN/END in csrc/common.h), so the library built here is
+the one an unmodified AKLR builds. The libraries go in-tree under ``aklr_amd/schema/_built/`` so that a
+GPU run loads what was built here, and ``op_schema_errors`` restates the builder's check of the op it
 registers (builder.py:309-323)."""
 from __future__ import annotations
 
@@ -17,7 +18,7 @@ from . import text
 
 BUILT = Path(__file__).resolve().parent / "_built"
 ARCH = "gfx950"
-FLAGS = ["-O3", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+FLAGS = ["-O3"]
 
 
 def library_path(kernel: Mapping[str, Any], root: Path = BUILT) -> Path:

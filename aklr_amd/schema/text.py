@@ -1,3 +1,9 @@
+# SPDX-License-Identifier: MIT
+# Copyright (C) 2026, Advanced Micro Devices, Inc. All rights reserved.
+# The formats here follow aklr/core/contract/expr.py:108-136 (the schema text),
+# aklr/core/contract/locate.py:114-118 and aklr/core/contract/spec/_kernel.py:152-161 (the uuid and
+# content hash), whose licence notice this is.
+
 """The text and the name of an AKLR schema file.
 
 A schema file is named by a hash of what its author wrote, and its text has one canonical form; an

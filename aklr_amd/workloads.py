@@ -88,3 +88,29 @@ def zipf_routing(tokens: int, experts: int = 256, top_k: int = 8, *, alpha: floa
     p = torch.arange(1, experts + 1, dtype=torch.float64).pow(-alpha)
     ids = torch.multinomial(p.expand(tokens, experts), top_k, replacement=False, generator=g)
     return ids.to(device)
+
+
+def moe_expert_weights(experts: int, rows: int, cols: int, *, seed: int = 1, device="cpu", std: float = 0.02):
+    """Stacked expert weights of the MoE configuration: per expert, fp32 ~ N(0, std) [rows, cols]
+    quantized per 128x128 block to e4m3fn with s = amax / 448, as blockwise_fp8_weight. Returns (codes
+    e4m3fn [experts, rows, cols], fp32 scales [experts, ceil(rows/128), cols/128]); expert e draws from
+    seed + e."""
+    codes = torch.empty((experts, rows, cols), dtype=torch.float8_e4m3fn, device=device)
+    scales = torch.empty((experts, -(-rows // 128), cols // 128), dtype=torch.float32, device=device)
+    for e in range(experts):
+        c, s = blockwise_fp8_weight(rows, cols, seed=seed + e, device=device, std=std)
+        codes[e].copy_(c)
+        scales[e].copy_(s)
+    return codes, scales
+
+
+def moe_routing(tokens: int, experts: int = 256, top_k: int = 8, *, seed: int = 3, device="cpu"):
+    """Config-5 routing as the experts take it: Zipf(1.1) ids [tokens, top_k] plus the shared expert
+    (id ``experts``) in the last slot, int32; weights fp32 [tokens, top_k + 1] ~ U(0, 1), the shared
+    slot at 1."""
+    ids = zipf_routing(tokens, experts, top_k, seed=seed, device="cpu").to(torch.int32)
+    ids = torch.cat([ids, torch.full((tokens, 1), experts, dtype=torch.int32)], 1)
+    g = generator(seed + 1, "cpu")
+    wts = torch.rand((tokens, top_k + 1), generator=g)
+    wts[:, -1] = 1.0
+    return ids.to(device), wts.to(device)

@@ -260,12 +260,23 @@ REFERENCE_RECORDED = [
 ]
 
 
+REFERENCE_TRACE_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                    "reference_recorded_fp8_kernel_trace.json")
+
+
 def reference_recorded_figures(dev, stream, steps=7):
     """This build's gemm_a8w8_blockwise_scaled on the shapes the reference records CI times for, each
-    call on cold caches (the graph rotates over > 512 MB of operand copies)."""
+    call on cold caches (the graph rotates over > 512 MB of operand copies). Beside each event-timed
+    figure: the median kernel duration from the committed rocprofv3 kernel trace of
+    ``bench.py --probe-reference`` (the kind of figure the reference's tracer records), when present."""
     import aklr_amd
     from aklr_amd import layouts, workloads
 
+    try:
+        with open(REFERENCE_TRACE_FILE) as f:
+            traced = {(r["m"], r["n"], r["k"], r["variant"]): r for r in json.load(f)["shapes"]}
+    except (OSError, ValueError, KeyError):
+        traced = {}
     out = []
     for (m, n, k, variant, ref_us, src) in REFERENCE_RECORDED:
         copies = []
@@ -292,6 +303,9 @@ def reference_recorded_figures(dev, stream, steps=7):
         out.append({"m": m, "n": n, "k": k, "variant": variant, "us": round(t, 2), "reference_us": ref_us,
                     "speedup": round(ref_us / t, 3), "tflops": round(tf, 1),
                     "gbs": round(gemm8_bytes(m, n, k) / (t * 1e-6) / 1e9, 1), "reference_source": src})
+        tr = traced.get((m, n, k, variant))
+        if tr is not None:
+            out[-1].update(kernel_trace_us=tr["kernel_us"], speedup_kernel_trace=round(ref_us / tr["kernel_us"], 3))
         torch.cuda.empty_cache()
     return out
 
@@ -488,6 +502,7 @@ def probe_prefill(dev, stream, calls=6):
     from aklr_amd import layouts, workloads
 
     m = 4096
+    plan = []
     for (n, k) in workloads.DEEPSEEK_NK:
         copies = []
         for r in range(_copies(gemm8_bytes(m, n, k), lo=2)):
@@ -501,8 +516,140 @@ def probe_prefill(dev, stream, calls=6):
             aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s, bs, operand_format="none:preshuffled")
         torch.cuda.synchronize()
         print(f"[bench] prefill probe m={m} n={n} k={k}: {len(copies) + calls} calls", file=sys.stderr, flush=True)
+        plan.append({"case": "fp8_lds_m4096", "m": m, "n": n, "k": k, "kernels": ["gemm8_lds_kernel"],
+                     "launches": len(copies) + calls, "warm": len(copies)})
         del copies
         torch.cuda.empty_cache()
+    _calibration_copy(dev)
+    print("[bench] probe plan " + json.dumps(plan), file=sys.stderr, flush=True)
+
+
+def _calibration_copy(dev):
+    """A plain 256 MiB device copy, three times: what FETCH_SIZE and WRITE_SIZE read for 268,435,456
+    bytes moved scales the GEMMs' readings in the same profiler run."""
+    src = torch.empty(256 * 2**20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    print("[bench] calibration copy: 3 x 268435456 bytes", file=sys.stderr, flush=True)
+
+
+def probe_counters(dev, stream, calls=4):
+    """The program the per-kernel counter summaries are read on (rocprofv3 --pmc / --kernel-trace). Every
+    case runs its GEMM once per rotating cold operand copy (> 512 MB in all) and then ``calls`` more
+    times; the calibration copy ends the run. Cases, in launch order:
+      fp8_lds_m1024      FP8 LDS kernel, M=1024 on the three DeepSeek-V3 shapes
+      fp8_stream_m64/128 FP8 stream kernel at M=64 and 128 on the DeepSeek-V3 shapes and on 7168x2048
+      mxfp4_lds          MXFP4 LDS kernel at M=512 and 4096 on the three Llama-3-70B shapes
+      moe_t4096          the grouped MoE experts at T=4096 (Zipf(1.1) top-8 + shared; the gate-up and
+                         the down launch are moe_gemm_kernel<true, ...> and <false, ...>)
+    A JSON line on stderr lists each case with its kernel-name patterns and its number of launches of each
+    (the MoE's gate-up and down launches alternate), in order, so a parser can assign the profiler's
+    dispatches to cases."""
+    import aklr_amd
+    from aklr_amd import layouts, workloads
+
+    plan = []
+
+    def fp8_case(tag, m, n, k, kernel):
+        copies = []
+        for r in range(_copies(gemm8_bytes(m, n, k), lo=2)):
+            x = workloads.activations(m, k, seed=1 + r, device=dev)
+            q, s = aklr_amd.per_group_quant_fp8(x)
+            b, bs = workloads.blockwise_fp8_weight(n, k, seed=2 + r, device=dev)
+            copies.append((q, s.view(m, k // 128), layouts.shuffle_weight(b), bs))
+            del x, b
+        torch.cuda.synchronize()
+        for i in range(len(copies) + calls):
+            q, s, b, bs = copies[i % len(copies)]
+            aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s, bs, operand_format="none:preshuffled")
+        torch.cuda.synchronize()
+        plan.append({"case": tag, "m": m, "n": n, "k": k, "kernels": [kernel], "launches": len(copies) + calls,
+                     "warm": len(copies)})
+        print(f"[bench] counters probe {tag} m={m} n={n} k={k}", file=sys.stderr, flush=True)
+        del copies
+        torch.cuda.empty_cache()
+
+    for (n, k) in workloads.DEEPSEEK_NK:
+        fp8_case("fp8_lds_m1024", 1024, n, k, "gemm8_lds_kernel")
+    for m in (64, 128):
+        for (n, k) in workloads.DEEPSEEK_NK + ((7168, 2048),):
+            fp8_case(f"fp8_stream_m{m}", m, n, k, "gemm8_stream_kernel")
+
+    for m in (512, 4096):
+        for (n, k) in workloads.LLAMA70B_NK:
+            copies = []
+            for r in range(_copies(gemm4_bytes(m, n, k), lo=2)):
+                x = workloads.activations(m, k, seed=1 + r, device=dev)
+                qa, sa = aklr_amd.dynamic_mxfp4_quant(x, shuffle=True)
+                wb, sb = workloads.mxfp4_weight(n, k, seed=10 + r, device=dev)
+                copies.append((qa, sa, layouts.shuffle_weight(wb), layouts.e8m0_scales(sb)))
+                del x, wb
+            torch.cuda.synchronize()
+            for i in range(len(copies) + calls):
+                qa, sa, wb, sb = copies[i % len(copies)]
+                aklr_amd.gemm_a4w4_mxfp4(qa, wb, sa, sb)
+            torch.cuda.synchronize()
+            plan.append({"case": "mxfp4_lds", "m": m, "n": n, "k": k, "kernels": ["gemm4_lds_kernel"],
+                         "launches": len(copies) + calls, "warm": len(copies)})
+            print(f"[bench] counters probe mxfp4 m={m} n={n} k={k}", file=sys.stderr, flush=True)
+            del copies
+            torch.cuda.empty_cache()
+
+    e, d, inter, topk, t = 256, 7168, 2048, 8, 4096
+    w1, s1 = workloads.moe_expert_weights(e + 1, 2 * inter, d, seed=20, device=dev)
+    w2, s2 = workloads.moe_expert_weights(e + 1, d, inter, seed=21, device=dev)
+    x = workloads.activations(t, d, seed=22, device=dev, outliers=False)
+    ids, wts = workloads.moe_routing(t, e, topk, seed=23, device=dev)
+    moe_calls = 1 + calls
+    for _ in range(moe_calls):
+        aklr_amd.moe_fp8_experts(x, w1, w2, wts, ids, s1, s2)
+    torch.cuda.synchronize()
+    plan.append({"case": "moe_t4096", "tokens": t, "kernels": ["moe_gemm_kernel<0,", "moe_gemm_kernel<1,"],
+                 "launches": moe_calls, "warm": 1})
+    print("[bench] counters probe moe t=4096", file=sys.stderr, flush=True)
+    del w1, w2, s1, s2
+    torch.cuda.empty_cache()
+    _calibration_copy(dev)
+    print("[bench] probe plan " + json.dumps(plan), file=sys.stderr, flush=True)
+
+
+def probe_reference(dev, stream, calls=5):
+    """The program the kernel-trace comparison with the reference's recorded times is read on: this
+    build's FP8 GEMM on each of the reference's 17 recorded shapes, once per rotating cold operand copy
+    and then ``calls`` more times (rocprofv3 --kernel-trace gives each launch's duration, the kind of
+    figure the reference's own tracer records)."""
+    import aklr_amd
+    from aklr_amd import layouts, workloads
+
+    plan = []
+    for (m, n, k, variant, ref_us, src) in REFERENCE_RECORDED:
+        copies = []
+        for r in range(_copies(gemm8_bytes(m, n, k), lo=2)):
+            x = workloads.activations(m, k, seed=300 + r, device=dev)
+            q, s = aklr_amd.per_group_quant_fp8(x)
+            b, bs = workloads.blockwise_fp8_weight(n, k, seed=400 + r, device=dev)
+            if variant == "b_shuffled":
+                copies.append((q, s.view(m, k // 128), layouts.shuffle_weight(b), bs))
+            else:
+                copies.append((q, s.view(k // 128, m).t().contiguous(), b, bs))
+            del x, b
+        torch.cuda.synchronize()
+        for i in range(len(copies) + calls):
+            q, s, b, bs = copies[i % len(copies)]
+            if variant == "b_shuffled":
+                aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s, bs, operand_format="none:preshuffled")
+            else:
+                aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s, bs)
+        torch.cuda.synchronize()
+        plan.append({"case": f"{m}x{n}x{k} {variant}", "m": m, "n": n, "k": k, "variant": variant,
+                     "reference_us": ref_us, "kernels": ["gemm8_"], "launches": len(copies) + calls,
+                     "warm": len(copies)})
+        del copies
+        torch.cuda.empty_cache()
+    print("[bench] probe plan " + json.dumps(plan), file=sys.stderr, flush=True)
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
@@ -526,11 +673,10 @@ def probe_traffic(dev, stream):
     for _ in range(3):
         for b, bs in copies:
             aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s.view(m, k // 128), bs, operand_format="none:preshuffled")
-    src = torch.empty(256 * 2**20, dtype=torch.uint8, device=dev).fill_(1)
-    dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
+    _calibration_copy(dev)
+    print("[bench] probe plan " + json.dumps([{"case": "fp8_stream_m16", "m": m, "n": n, "k": k,
+                                               "kernels": ["gemm8_stream_kernel"], "launches": 24, "warm": 0}]),
+          file=sys.stderr, flush=True)
     print("[bench] traffic probe done", file=sys.stderr, flush=True)
 
 
@@ -578,10 +724,19 @@ def cpu_baseline():
         cores = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
     except Exception:  # noqa: BLE001
         cores = os.cpu_count() or 1
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), None)
+    except OSError:
+        pass
     return {
         "value": round(total_bytes / dt / 1e9, 3),
         "unit": "GB/s",
         "cores": int(cores),
+        "cpu_count": os.cpu_count(),
+        "torch_threads": torch.get_num_threads(),
+        "cpu_model": model,
         "kind": "port",
         "sample": f"one decode step, M in {{1,4,16,64,128}} x (N,K) in (2112,7168),(24576,1536),(7168,16384): "
                   f"quant + dequant + fp32 matmul, median of 3 reps ({', '.join(f'{r:.2f}' for r in reps)} s)",
@@ -603,6 +758,12 @@ def main(argv=None):
     ap.add_argument("--probe-floor", action="store_true",
                     help="only time the decode floors: an empty kernel and a pure HBM read of each decode "
                          "shape's bytes, beside the GEMM (for rocprofv3 --kernel-trace)")
+    ap.add_argument("--probe-counters", action="store_true",
+                    help="only run the per-kernel counter cases (FP8 LDS at M=1024, FP8 stream at M=64/128, "
+                         "MXFP4 LDS at M=512/4096, MoE at T=4096) and a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--probe-reference", action="store_true",
+                    help="only run the FP8 GEMM on the reference's 17 recorded shapes (for rocprofv3 "
+                         "--kernel-trace)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -620,6 +781,12 @@ def main(argv=None):
     if args.probe_prefill:
         probe_prefill(dev, stream)
         return 0
+    if args.probe_counters:
+        probe_counters(dev, stream)
+        return 0
+    if args.probe_reference:
+        probe_reference(dev, stream)
+        return 0
     if args.probe_floor:
         step_fn, n_sets, step_bytes, weights, xs = build_decode(dev, True)
         print(json.dumps(decode_floor_figures(dev, stream, weights)), flush=True)
@@ -627,6 +794,7 @@ def main(argv=None):
     shuffled = args.layout == "preshuffled"
     print(f"[bench] building decode workload ({args.layout})", file=sys.stderr, flush=True)
     step_fn, n_sets, step_bytes, weights, xs = build_decode(dev, shuffled)
+    copies_per_shape = {nk: len(c) for nk, c in weights.items()}
     graphs = [_capture(step_fn(r), stream) for r in range(n_sets)]
     print(f"[bench] {len(graphs)} step graphs captured; timing {args.steps} steps", file=sys.stderr, flush=True)
     ms_per_step = _replay_time_ms(graphs, args.steps, args.warmup, stream)
@@ -691,7 +859,8 @@ def main(argv=None):
             "workload": "deepseek_v3_decode_fp8_blockscale: M in {1,4,16,64,128} x (N,K) in "
                         "{(2112,7168),(24576,1536),(7168,16384)}, quant + GEMM per step",
             "b_layout": args.layout,
-            "weight_copies_rotated": n_sets,
+            "weight_copies_per_shape": {f"{n}x{k}": c for (n, k), c in copies_per_shape.items()},
+            "step_graphs": n_sets,
             "step_bytes": step_bytes,
         },
         "roofline": {

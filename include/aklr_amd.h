@@ -135,6 +135,15 @@ int aklr_gemm_a8w8_blockscale_noalloc(const void* a, int64_t lda, const void* b,
                                       int fp8_dtype, int b_layout, int out_dtype, hipStream_t stream);
 
 /*
+ * The current device's copy of the no-allocation array: *ptr receives its device address and *bytes
+ * its size (AKLR_NOALLOC_SCRATCH_BYTES). No counterpart in the reference; it lets a caller of
+ * aklr_gemm_a8w8_blockscale_noalloc (one that cannot allocate) see the memory those calls share, e.g.
+ * to check that a finished call left no split-K arrival word tagged. Allocates nothing; the same
+ * once-per-device address lookup as the entry point's.
+ */
+int aklr_noalloc_scratch(void** ptr, size_t* bytes);
+
+/*
  * Byte transpose dst[c][r] = src[r][c] for a [rows, cols] matrix of 8-bit codes (row strides src_ld,
  * dst_ld in bytes). It serves gemm_a8w8_blockwise_scaled with trans_b = false, where b is (k, n)
  * (aklr/ops/gemm/contract.py:61-76 `_TRANS_B`, aklr/ops/gemm/reference.py:32-37 `_weight`: b.mT): the

@@ -323,3 +323,23 @@ def test_built_libraries_register_the_call_keys(contract_id, variant):
     c = S.CONTRACTS[contract_id]
     op = build.load(kernel)
     assert build.op_schema_errors(op.default._schema, c.call_keys, c.mutable) == []
+
+
+def test_kernel_sources_switch_packed_fp32_off():
+    """AKLR builds the packaged sources with -O3 only, so each kernel source must switch packed fp32 VALU
+    ops off itself: AKLR_SCALAR_FP32_BEGIN after its last include and AKLR_SCALAR_FP32_END as its last
+    line (common.h wraps its own functions the same way)."""
+    from pathlib import Path
+
+    csrc = Path(__file__).resolve().parent.parent / "aklr_amd" / "csrc"
+    files = sorted(csrc.glob("*.hip")) + [csrc / "common.h"]
+    assert len(files) >= 7
+    for f in files:
+        lines = [ln for ln in f.read_text().splitlines() if ln.strip()]
+        begin = [i for i, ln in enumerate(lines) if ln == "AKLR_SCALAR_FP32_BEGIN"]
+        end = [i for i, ln in enumerate(lines) if ln == "AKLR_SCALAR_FP32_END"]
+        assert len(begin) == 1 and len(end) == 1, f"{f.name}: one BEGIN and one END"
+        last_include = max(i for i, ln in enumerate(lines) if ln.startswith("#include"))
+        assert begin[0] > last_include, f"{f.name}: BEGIN comes after the includes"
+        if f.suffix == ".hip":
+            assert end[0] == len(lines) - 1, f"{f.name}: END is the last line"
