@@ -524,10 +524,13 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
 
 // ---------------------------------------------------------------------------------------------
 // lds (m > 128): TM x TN workgroup tiles, 8 waves in 2 (m) x 4 (n) -- 4 x 2 for TN = 224 -- each wave
-// (TM/WM) x (TN/WN), K steps of 128 through an S-stage LDS ring that S - 1 stages fill ahead of the
-// compute. A, B and a_scale go global -> LDS with direct-to-LDS buffer loads (no register staging),
-// every wave issuing the same number of loads per stage, so one immediate wait count leaves exactly
-// S - 2 stages in flight.
+// (TM/WM) x (TN/WN), K steps of 128 through LDS rings of SA stages of A (with the step's a_scale column
+// and b_scale row) and SB stages of B, filled by direct-to-LDS buffer loads (no register staging): A runs
+// SA - 1 stages ahead of the compute and B SB - 1. With SA = SB + 1, A -- the operand whose lines miss
+// L2 more often in the XCD tile order below (each A row block serves 4 resident tiles of an XCD, each B
+// column block 8) -- gets one stage more latency to hide than B in the same LDS. Every wave issues the
+// same number of loads per stage, so one immediate wait count per step leaves exactly the younger stages
+// in flight.
 // Each LDS operand tile is rows of 128 bytes with the 16-byte chunks XOR-swizzled by row (chunk c of
 // row r at position c ^ (r & 7)): lane i of a load writes position i % 8 of row i / 8 of its 8-row
 // slab and so fetches chunk (i % 8) ^ (r & 7) of that row; the MFMA fragment reads (row li, chunks
@@ -539,9 +542,14 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
 // Buffer descriptors start at the workgroup's own tile, so 32-bit offsets cover any matrix size.
 constexpr int kLdsGroup = 8;  // tile rows per raster group
 
-template <int TM, int TN, int S, int FMT, bool PRE>
+// LDS bytes of an A stage (codes, a_scale column, b_scale row) and of a B stage of a TM x TN tile.
+__host__ __device__ constexpr int lds8_stage_a(int tm) { return tm * 128 + (tm + 64) * 4; }
+__host__ __device__ constexpr int lds8_stage_b(int tn) { return tn * 128; }
+
+template <int TM, int TN, int SA, int SB, int FMT, bool PRE>
 __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
-  static_assert(TM % 64 == 0 && (TN == 128 || TN == 192 || TN == 224 || TN == 256) && S >= 2, "tile shape");
+  static_assert(TM % 64 == 0 && TM <= 256 && (TN == 128 || TN == 192 || TN == 224 || TN == 256), "tile shape");
+  static_assert(SB >= 2 && (SA == SB || SA == SB + 1), "stage counts");
   constexpr int WN = TN == 224 ? 2 : 4, WM = 8 / WN;  // waves along n and m
   constexpr int MT = TM / (16 * WM), NT = TN / (16 * WN);  // 16x16 tiles per wave along m and n
   // TN = 192 (N = 2112 = 11 x 192) and 224 (N = 7168 = 32 x 224): tiles start at multiples of 64 or
@@ -549,15 +557,21 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   constexpr bool kBlkPerTile = TN % 128 != 0;
   constexpr int kNBlk = TN == 224 ? 3 : (TN + 127) / 128;  // 128-column b_scale blocks a tile spans
   // B moves in slabs of 8 rows, BI per wave. When the slabs do not divide evenly (TN = 224: 28 slabs),
-  // wave w takes slabs w, w + 8, ... and the slots past TN issue an empty load into the stage's spare
-  // rows, so every wave's count stays the same.
+  // wave w takes slabs w, w + 8, ... and the slots past TN issue an empty load into a shared landing
+  // area, so every wave's count stays the same.
   constexpr int kSlabsB = TN / 8;
   constexpr int BI = (kSlabsB + 7) / 8;
   constexpr bool kEvenB = kSlabsB % 8 == 0;
   constexpr int AI = TM / 64;                // 1 KiB A loads per wave per stage
-  constexpr int kLoads = AI + BI + 1;        // + one a_scale load
-  constexpr int kStageA = TM * 128, kStageB = BI * 8 * 1024;
-  constexpr int kScaleWaves = TM / 64;       // waves whose a_scale load carries rows
+  constexpr int kLoadsA = AI + 1;            // + one scale load (a_scale rows, b_scale row, or empty)
+  constexpr int kLoads = kLoadsA + BI;
+  constexpr int kStageA = TM * 128, kStageB = lds8_stage_b(TN);
+  constexpr int kScaleWaves = TM / 64;       // waves whose scale load carries a_scale rows
+  constexpr int kSStride = TM + 64;          // floats per stage: a_scale rows, then b_scale blocks
+  // Loads still in flight at a step's wait: the younger stages. With SA = SB + 1 each step issues B of
+  // stage kb + SB - 1 and then A of stage kb + SA - 1 = kb + SB, so when step kb needs A(kb) and B(kb),
+  // what was issued after B(kb) is A(kb + 1) and the SB - 2 whole steps after that.
+  constexpr int kInFlight = SA == SB ? (SB - 2) * kLoads : (SB - 2) * kLoads + kLoadsA;
   // Each MFMA's fold runs kLag MFMAs after it (the last kLag of a step at the start of the next), so
   // its FMAs read a result that is already complete and issue while the matrix core works on later
   // tiles; folding the newest result instead stalls every step on the MFMA latency (measured 8-10%
@@ -565,11 +579,11 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   constexpr int kLag = 3;
   constexpr int kT = MT * NT;
   static_assert(kT > kLag, "fold lag");
-  __shared__ __attribute__((aligned(1024))) uint8_t sA[S * kStageA];
-  __shared__ __attribute__((aligned(1024))) uint8_t sB[S * kStageB];
-  __shared__ __attribute__((aligned(16))) float sS[S * TM];
-  __shared__ __attribute__((aligned(16))) float sDummy[8 * 64];  // landing area of the empty a_scale loads
-  __shared__ float sSB[kNBlk][512];  // b_scale of the tile's 128-column blocks over its K range
+  static_assert(kScaleWaves < 8, "a wave left for the b_scale row");
+  __shared__ __attribute__((aligned(1024))) uint8_t sA[SA * kStageA];
+  __shared__ __attribute__((aligned(1024))) uint8_t sB[SB * kStageB];
+  __shared__ __attribute__((aligned(16))) float sS[SA * kSStride];
+  __shared__ __attribute__((aligned(16))) uint8_t sDummy[1024];  // landing area of the empty loads
   __shared__ unsigned arrive_slot;
 
   const int tiles_m = (p.m + TM - 1) / TM;
@@ -599,18 +613,22 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   if (p.splits > 1 && w == 0) seen = splitk_peek(p.counters + pid);
 
   // Wave w moves rows [w*TM/8, (w+1)*TM/8) of the A tile and its BI slabs of the B tile, in slabs of 8
-  // rows; waves below kScaleWaves move a_scale rows [64w, 64w + 64), the others issue an empty load so
-  // that every wave's count per stage is kLoads.
+  // rows. Its scale load: waves below kScaleWaves move a_scale rows [64w, 64w + 64); wave kScaleWaves
+  // moves the b_scale of the tile's kNBlk column blocks (lane r: block n0 / 128 + r, clamped to the last
+  // row of b_scale); the others issue an empty load. Every wave's count per stage is kLoads.
   const i32x4 ars = make_rsrc_words(p.a + (int64_t)m0 * p.lda, rsrc_bytes((int64_t)(p.m - 1 - m0) * p.lda + p.k));
   const int64_t b_base = PRE ? (int64_t)(n0 >> 4) * kt32 * 512 : (int64_t)n0 * p.ldb;
   const int64_t b_total = PRE ? (int64_t)p.n * p.k : (int64_t)(p.n - 1) * p.ldb + p.k;
   const i32x4 brs = make_rsrc_words(p.b + b_base, rsrc_bytes(b_total - b_base));
-  const i32x4 sars = make_rsrc_words(
-      p.sa + (int64_t)m0 * p.sa_sm,
-      rsrc_bytes(((int64_t)(p.m - 1 - m0) * p.sa_sm + (int64_t)(KB - 1) * p.sa_sk + 1) * 4));
+  const int last_row = (p.n - 1) >> 7;
+  const bool a_scale_wave = w < kScaleWaves, b_scale_wave = w == kScaleWaves;
+  const i32x4 srs =
+      a_scale_wave ? make_rsrc_words(p.sa + (int64_t)m0 * p.sa_sm,
+                                     rsrc_bytes(((int64_t)(p.m - 1 - m0) * p.sa_sm + (int64_t)(KB - 1) * p.sa_sk + 1) * 4))
+                   : make_rsrc_words(p.sb, rsrc_bytes(((int64_t)last_row * p.ldbs + KB) * 4));
   const int lr = lane >> 3, lp = lane & 7;  // row within the slab, LDS chunk position
   const int c = lp ^ lr;                     // every slab starts at a multiple of 8 rows
-  uint32_t a_off[AI], b_off[BI];
+  uint32_t a_off[AI], b_off[BI], b_lds[BI], b_lds_step[BI];
 #pragma unroll
   for (int j = 0; j < AI; ++j) {
     const int r = w * (TM / 8) + j * 8 + lr;
@@ -618,8 +636,11 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   }
 #pragma unroll
   for (int j = 0; j < BI; ++j) {
-    const int slab = kEvenB ? w * BI + j : w + 8 * j;
+    const int slab = kEvenB ? w * BI + j : w + 8 * j;  // wave-uniform
     const int r = slab * 8 + lr;
+    // the LDS targets go to m0 through an SGPR: readfirstlane makes their uniformity explicit
+    b_lds[j] = __builtin_amdgcn_readfirstlane(slab < kSlabsB ? lds_addr(&sB[slab * 1024]) : lds_addr(sDummy));
+    b_lds_step[j] = slab < kSlabsB ? kStageB : 0;
     if (slab >= kSlabsB)
       b_off[j] = kOobOffset;
     else if (PRE)
@@ -628,30 +649,40 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
     else
       b_off[j] = n0 + r < p.n ? (uint32_t)(r * p.ldb + c * 16) : kOobOffset;
   }
-  const bool scale_wave = w < kScaleWaves;
-  const uint32_t sa_off =
-      scale_wave && m0 + w * 64 + lane < p.m ? (uint32_t)((w * 64 + lane) * p.sa_sm * 4) : kOobOffset;
+  uint32_t s_off = kOobOffset, s_kstep = 0, lds_s = lds_addr(sDummy), lds_s_step = 0;
+  if (a_scale_wave) {
+    if (m0 + w * 64 + lane < p.m) s_off = (uint32_t)((w * 64 + lane) * p.sa_sm * 4);
+    s_kstep = (uint32_t)(p.sa_sk * 4);
+    lds_s = lds_addr(&sS[w * 64]);
+    lds_s_step = kSStride * 4;
+  } else if (b_scale_wave) {
+    if (lane < kNBlk) s_off = (uint32_t)((int64_t)min((n0 >> 7) + lane, last_row) * p.ldbs * 4);
+    s_kstep = 4;
+    lds_s = lds_addr(&sS[TM]);
+    lds_s_step = kSStride * 4;
+  }
+  lds_s = __builtin_amdgcn_readfirstlane(lds_s);
+  lds_s_step = __builtin_amdgcn_readfirstlane(lds_s_step);
   const uint32_t lds_a = lds_addr(&sA[w * (TM / 8) * 128]);
-  const uint32_t lds_b = lds_addr(&sB[(kEvenB ? w * BI : w) * 1024]);
-  constexpr uint32_t kSlabStrideB = kEvenB ? 1024 : 8 * 1024;  // LDS bytes between a wave's B slabs
-  const uint32_t lds_s = scale_wave ? lds_addr(&sS[w * 64]) : lds_addr(&sDummy[w * 64]);
-  const uint32_t lds_s_step = scale_wave ? TM * 4 : 0;
-  const uint32_t sa_kstep = (uint32_t)(p.sa_sk * 4);
   // The lane offsets stay fixed; a stage's K offset rides soffset, so an issue is scalar work only.
   // A stage past the K range loads through a descriptor of no bytes: zeros, no memory traffic, and
   // the same load count.
-  auto issue = [&](int kb, int st) {
+  auto issue_a = [&](int kb, int st) {
     const bool on = kb < kb_end;
-    i32x4 ra = ars, rb = brs, rs = sars;
+    i32x4 ra = ars, rs = srs;
     ra[2] = on ? ars[2] : 0;
+    rs[2] = on ? srs[2] : 0;
+#pragma unroll
+    for (int j = 0; j < AI; ++j) lds_dma16_so(ra, lds_a + st * kStageA + j * 1024, a_off[j], (uint32_t)kb * 128u);
+    lds_dma4_so(rs, lds_s + st * lds_s_step, s_off, (uint32_t)kb * s_kstep);
+  };
+  auto issue_b = [&](int kb, int st) {
+    const bool on = kb < kb_end;
+    i32x4 rb = brs;
     rb[2] = on ? brs[2] : 0;
-    rs[2] = on ? sars[2] : 0;
-    const uint32_t ak = (uint32_t)kb * 128u, bk = PRE ? (uint32_t)kb * 2048u : (uint32_t)kb * 128u;
+    const uint32_t bk = PRE ? (uint32_t)kb * 2048u : (uint32_t)kb * 128u;
 #pragma unroll
-    for (int j = 0; j < AI; ++j) lds_dma16_so(ra, lds_a + st * kStageA + j * 1024, a_off[j], ak);
-#pragma unroll
-    for (int j = 0; j < BI; ++j) lds_dma16_so(rb, lds_b + st * kStageB + j * kSlabStrideB, b_off[j], bk);
-    lds_dma4_so(rs, lds_s + st * lds_s_step, sa_off, (uint32_t)kb * sa_kstep);
+    for (int j = 0; j < BI; ++j) lds_dma16_so(rb, b_lds[j] + st * b_lds_step[j], b_off[j], bk);
   };
 
   f32x4 acc[MT][NT];
@@ -660,24 +691,13 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // b_scale goes through LDS: a global load inside the loop (after its barriers) could not use the
-  // scalar unit and would be waited for together with the in-flight tile loads.
-  {
-    const int len = kb_end - kb_begin;
-    const int last_row = (p.n - 1) >> 7;
-    for (int i = threadIdx.x; i < kNBlk * len; i += 512) {
-      const int r = i / len, kk = i - r * len;
-      sSB[r][kk] = p.sb[(int64_t)min((n0 >> 7) + r, last_row) * p.ldbs + kb_begin + kk];
-    }
-  }
   // A wave's columns (at most 112) lie in at most two 128-column blocks: block blk0 and, from column
   // tile split_nt on, blk0 + 1. The K loop is instantiated per split_nt, so a step computes 2 * MT
   // scale products (a_scale x each block's b_scale) instead of one per MFMA.
   const int wcol = n0 + wn * (TN / WN);
   const int blk0 = (wcol >> 7) - (n0 >> 7);
   const int split_nt = min(NT, (128 - (wcol & 127)) >> 4);
-  const float* sb0 = sSB[blk0];
-  const float* sb1 = sSB[min(blk0 + 1, kNBlk - 1)];
+  const int sb_lo_i = TM + blk0, sb_hi_i = TM + min(blk0 + 1, kNBlk - 1);
 
   // Fragment addresses: every row a lane reads is congruent to li mod 8, so the swizzle term is the
   // same for all its row tiles and each read is one base plus an immediate (stage and tile offsets).
@@ -700,11 +720,12 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
 
   auto kloop = [&](auto split_c) {
     constexpr int SPLIT = decltype(split_c)::value;  // first column tile in block blk0 + 1 (NT: none)
-    auto compute = [&](int kb, auto st_c) {
-      constexpr int ST = decltype(st_c)::value;
-      const uint8_t* A = sA + ST * kStageA;
-      const uint8_t* B = sB + ST * kStageB;
-      const float* SA = sS + ST * TM + s_row;
+    auto compute = [&](auto sa_c, auto sb_c) {
+      constexpr int STA = decltype(sa_c)::value, STB = decltype(sb_c)::value;
+      const uint8_t* A = sA + STA * kStageA;
+      const uint8_t* B = sB + STB * kStageB;
+      const float* SS = sS + STA * kSStride;
+      const float* SA_ = SS + s_row;
       auto read_a = [&](int mt) {
         return cat(*reinterpret_cast<const u32x4*>(A + a_row + swz_lo + mt * 2048),
                    *reinterpret_cast<const u32x4*>(A + a_row + swz_hi + mt * 2048));
@@ -716,12 +737,12 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
       i32x8 held[kHeld];
 #pragma unroll
       for (int i = 0; i < kHeld; ++i) held[i] = kHoldA ? read_a(i) : read_b(i);
-      const float sb_lo = sb0[kb - kb_begin];
-      const float sb_hi = SPLIT < NT ? sb1[kb - kb_begin] : 0.f;
+      const float sb_lo = SS[sb_lo_i];
+      const float sb_hi = SPLIT < NT ? SS[sb_hi_i] : 0.f;
       float sc_lo[MT], sc_hi[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const float sa_row = SA[mt * 16];
+        const float sa_row = SA_[mt * 16];
         sc_lo[mt] = sa_row * sb_lo;
         sc_hi[mt] = SPLIT < NT ? sa_row * sb_hi : 0.f;
       }
@@ -769,31 +790,39 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
         pend_s[j] = sc[kT - kLag + j];
       }
     };
-    // Stage kb lives in slot (kb - kb_begin) % S. At each step this wave's loads of the stage about to
-    // be computed are waited for (S - 2 younger stages stay in flight), then the barrier makes every
-    // wave's loads visible and guarantees that no wave still reads the slot the next issue refills
-    // (the slot computed one step earlier). The loop runs whole rounds of S steps, so every slot
-    // index is a constant.
-    auto step = [&](int kb, auto st_c) {
-      constexpr int ST = decltype(st_c)::value;
-      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((S - 2) * kLoads) : "memory");
+    // Stage kb lives in A slot (kb - kb_begin) % SA and B slot (kb - kb_begin) % SB. At each step this
+    // wave's loads of the stage about to be computed are waited for (the younger stages stay in
+    // flight), then the barrier makes every wave's loads visible and guarantees that no wave still reads
+    // the slots the issues refill (those of the stage computed one step earlier). The loop runs whole
+    // rounds of SA * SB / gcd steps, so every slot index is a constant.
+    auto step = [&](int kb, auto j_c) {
+      constexpr int J = decltype(j_c)::value;
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kInFlight) : "memory");
       __syncthreads();
-      issue(kb + S - 1, (ST + S - 1) % S);
-      compute(kb, st_c);
+      issue_b(kb + SB - 1, (J + SB - 1) % SB);
+      issue_a(kb + SA - 1, (J + SA - 1) % SA);
+      compute(IC<J % SA>{}, IC<J % SB>{});
     };
+    constexpr int kRound = SA == SB ? SA : SA * SB;  // SA = SB + 1: coprime
     int kb = kb_begin;
-    for (; kb + S <= kb_end; kb += S) {
+    for (; kb + kRound <= kb_end; kb += kRound) {
       auto ring = [&](auto j) { step(kb + decltype(j)::value, j); };
-      SFor<0, S>::run(ring);
+      SFor<0, kRound>::run(ring);
     }
     auto tail = [&](auto j) {
       if (kb + decltype(j)::value < kb_end) step(kb + decltype(j)::value, j);
     };
-    SFor<0, S - 1>::run(tail);
+    SFor<0, kRound - 1>::run(tail);
   };
 
+  // Prologue, in the steady state's issue order: with SA = SB + 1, A(0) and then (B(j), A(j + 1)) for
+  // j < SB - 1; with SA = SB, (B(j), A(j)) for j < SB - 1.
+  if constexpr (SA == SB + 1) issue_a(kb_begin, 0);
 #pragma unroll
-  for (int s = 0; s < S - 1; ++s) issue(kb_begin + s, s);
+  for (int j = 0; j < SB - 1; ++j) {
+    issue_b(kb_begin + j, j);
+    issue_a(kb_begin + j + SA - SB, j + SA - SB);
+  }
   if constexpr (!kBlkPerTile) {
     kloop(IC<NT>{});
   } else {
@@ -859,8 +888,8 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
     }
   }
 
-  // Output: whole-line stores through the ring's LDS, rows [0, TM/2) staged in sA and the rest in sB.
-  static_assert((TM / 2) * TN * 2 <= S * kStageA && (TM / 2) * TN * 2 <= S * kStageB, "output staging");
+  // Output: whole-line stores through the rings' LDS, rows [0, TM/2) staged in sA and the rest in sB.
+  static_assert((TM / 2) * TN * 2 <= SA * kStageA && (TM / 2) * TN * 2 <= SB * kStageB, "output staging");
   store_tile_via_lds<TM, TN, WM, WN, MT, NT>(acc, sA, sB, wm, wn, m0, n0, p.m, p.n, p.out, p.ldo, p.bias,
                                              p.out_dtype, p.nt_out != 0);
 }
@@ -1183,13 +1212,25 @@ static size_t quant_gemm_workspace(int64_t m, int64_t n, int64_t k) {
   return quant_codes_offset(m, n, k) + up256((size_t)m * k) + up256((size_t)(k / 128) * m * 4);
 }
 
-// Ring depth per tile shape: as many stages (at most 4) as 150 KiB of LDS holds.
-template <int TM, int TN, int FMT, bool PRE>
+// Ring depths per tile shape: as many stages (at most 4) of both operands as 150 KiB of LDS holds. The
+// 256x224 and 256x192 tiles run A one stage deeper (3 A, 2 B: 156.8 and 148.8 KiB), which fits only
+// because b_scale rides the A stages. Measured on cold operands, medians of interleaved runs (us, 2 -> 3
+// A stages, bitwise the same output): 256x224 at m = 4096 on 7168 x 16384 441.8 -> 432.7, at m = 8192
+// 865.6 -> 856.1; 256x192 at m = 4096 on 24576 x 1536 210.5 -> 205.6 and at m = 1024 53.2 -> 52.3. The
+// other tiles have no room for it; 128x192 with 4 A stages against 3 measured 35.9 against 35.4 us at
+// m = 1024 on 2112 x 7168.
+__host__ __device__ constexpr int lds8_stages(int tm, int tn) {
+  return 150 * 1024 / (lds8_stage_a(tm) + lds8_stage_b(tn)) < 4 ? 150 * 1024 / (lds8_stage_a(tm) + lds8_stage_b(tn))
+                                                                 : 4;
+}
+__host__ __device__ constexpr bool lds8_fits(int tm, int tn, int sa, int sb) {
+  return sa * lds8_stage_a(tm) + sb * lds8_stage_b(tn) + 1024 + 16 <= 160 * 1024;
+}
+template <int TM, int TN, int FMT, bool PRE, int SA = lds8_stages(TM, TN), int SB = lds8_stages(TM, TN)>
 static void launch_lds_t(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
-  constexpr int kStage = (TM + (TN / 8 + 7) / 8 * 64) * 128 + TM * 4;
-  constexpr int S = 150 * 1024 / kStage < 4 ? 150 * 1024 / kStage : 4;
-  hipLaunchKernelGGL((gemm8_lds_kernel<TM, TN, S, FMT, PRE>), dim3((unsigned)(t.grid_x * t.splits)), dim3(512), 0, s,
-                     a);
+  static_assert(lds8_fits(TM, TN, SA, SB), "LDS budget");
+  hipLaunchKernelGGL((gemm8_lds_kernel<TM, TN, SA, SB, FMT, PRE>), dim3((unsigned)(t.grid_x * t.splits)), dim3(512),
+                     0, s, a);
 }
 
 template <int FMT, bool PRE>
@@ -1198,8 +1239,8 @@ static void launch_lds(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
     launch_lds_t<192, 192, FMT, PRE>(a, t, s);
   } else if (t.tm == 256) {
     if (t.tn == 256) launch_lds_t<256, 256, FMT, PRE>(a, t, s);
-    else if (t.tn == 224) launch_lds_t<256, 224, FMT, PRE>(a, t, s);
-    else if (t.tn == 192) launch_lds_t<256, 192, FMT, PRE>(a, t, s);
+    else if (t.tn == 224) launch_lds_t<256, 224, FMT, PRE, 3, 2>(a, t, s);
+    else if (t.tn == 192) launch_lds_t<256, 192, FMT, PRE, 3, 2>(a, t, s);
     else launch_lds_t<256, 128, FMT, PRE>(a, t, s);
   } else {
     if (t.tn == 256) launch_lds_t<128, 256, FMT, PRE>(a, t, s);

@@ -9,15 +9,20 @@ last at weight 1).
   cover the 64-, 128- and 256-row block classes (and full 256-row blocks with remainders).
 - The whole op (router, grouped top-k, experts) at the same dimensions, with router inputs whose
   products are exact in fp32 so both sides route alike.
-- The full config-5 call (256 routed experts, T = 4096, 257 expert slots, Zipf(1.1) routing, the
-  610 MiB workspace layout) by two properties: relabelling the routed experts (weights, scales and ids
-  permuted together) leaves the output bit-identical, and sampled tokens match the oracle computed
-  from only those tokens' experts, copied to the host.
+- The full config-5 call (256 routed experts, T = 64 and T = 4096, 257 expert slots, Zipf(1.1) routing,
+  the 610 MiB workspace layout at T = 4096) by two properties: relabelling the routed experts (weights,
+  scales and ids permuted together) leaves the output bit-identical, and sampled tokens match the oracle
+  computed from only those tokens' experts, copied to the host.
+- The whole op at 256 routed experts with grouped top-k (8 groups, 4 kept) on router inputs whose
+  products are exact in fp32: sampled tokens against the oracle's routing (computed for every token on
+  the host) and their experts.
 - A call past the kernels' per-call token limit (32-bit offsets: 16644 tokens at 9 slots of 7168) runs
   as consecutive calls: its rows equal, bit for bit, a call on those rows alone.
 
-Weights are drawn on the GPU: N(0, 64) cast to e4m3fn (within +-448, as the contract's finite fp8
-draws), 128 x 128 block scales log-uniform in [2**-3, 1] / 512.
+The full-size calls draw BASELINE's weights: N(0, 0.02) per expert, block-quantized per 128 x 128 to
+e4m3fn with s = amax / 448 (workloads.moe_expert_weights). The smaller checks draw N(0, 64) cast to
+e4m3fn (within +-448, as the contract's finite fp8 draws) with 128 x 128 block scales log-uniform in
+[2**-3, 1] / 512, which spreads the scales over the fold's exponent range.
 """
 from __future__ import annotations
 
@@ -120,10 +125,30 @@ def test_deepseek_v2_fp8_moe_at_config5_dims():
     assert q >= 30.0
 
 
-def test_config5_full_call_relabel_and_sampled_tokens():
-    t, n_routed = 4096, 256
+def _baseline_weights(n_experts, seed):
+    """BASELINE configs[4]'s expert weights: N(0, 0.02), 128 x 128 block-quantized to e4m3fn."""
+    w1, s1 = workloads.moe_expert_weights(n_experts, 2 * INTER, D, seed=seed, device=DEV)
+    w2, s2 = workloads.moe_expert_weights(n_experts, D, INTER, seed=seed + 1000, device=DEV)
+    return w1, s1, w2, s2
+
+
+def _sampled_reference(toks, x, ids, w, w1, s1, w2, s2):
+    """The oracle output of tokens ``toks`` from only their own experts (host copies of those)."""
+    xs = f32(x[toks])
+    ref = np.zeros_like(xs)
+    for e in np.unique(ids[toks]).tolist():
+        hw1, hs1, hw2, hs2 = _host(w1[e], s1[e], w2[e], s2[e])
+        rows, slots = np.nonzero(ids[toks] == e)
+        y = moe.expert_mlp(xs[rows], hw1, hs1, hw2, hs2)
+        np.add.at(ref, rows, w[toks][rows, slots][:, None] * y)
+    return ref
+
+
+@pytest.mark.parametrize("t", [64, 4096])
+def test_config5_full_call_relabel_and_sampled_tokens(t):
+    n_routed = 256
     say(f"moe config 5 full call t={t} n_routed={n_routed}")
-    w1, s1, w2, s2 = _weights(n_routed + 1, seed=5)
+    w1, s1, w2, s2 = _baseline_weights(n_routed + 1, seed=5)
     x = workloads.activations(t, D, seed=6, device=DEV, outliers=False)
     ids, w = _zipf(t, n_routed, seed=7)
     tids, tw = torch.from_numpy(ids).to(DEV), torch.from_numpy(w).to(DEV)
@@ -143,16 +168,37 @@ def test_config5_full_call_relabel_and_sampled_tokens():
     assert torch.equal(out.view(torch.int16), out_p.view(torch.int16)), "relabelling the experts changed the output"
     del pw1, ps1, pw2, ps2
     # sampled tokens against the oracle, from their own <= 9 experts each
-    toks = [0, 1234, 2047, 4095]
-    xs = f32(x[toks])
-    got = f32(out[toks])
-    ref = np.zeros_like(xs)
-    for e in np.unique(ids[toks]).tolist():
-        hw1, hs1, hw2, hs2 = _host(w1[e], s1[e], w2[e], s2[e])
-        rows, slots = np.nonzero(ids[toks] == e)
-        y = moe.expert_mlp(xs[rows], hw1, hs1, hw2, hs2)
-        np.add.at(ref, rows, w[toks][rows, slots][:, None] * y)
-    q = moe.sqnr_db(formats.round_to_bf16(ref), got)
+    toks = [0, 1234, 2047, 4095] if t == 4096 else [0, 21, 42, 63]
+    ref = _sampled_reference(toks, x, ids, w, w1, s1, w2, s2)
+    q = moe.sqnr_db(formats.round_to_bf16(ref), f32(out[toks]))
+    say(f"  sampled tokens sqnr {q:.1f} dB")
+    assert q >= 30.0
+
+
+def test_deepseek_v2_fp8_moe_full_router_sampled_tokens():
+    # the whole op at config 5's expert count: router over 256 experts, grouped top-k (8 groups, 4 kept),
+    # renormalized weights x 2.5, the shared expert last; router products exact in fp32 (hidden in
+    # multiples of 1/16 within [-1, 1], router weights in {-1, 0, 1}/16), so GPU and host route alike
+    t, n_routed, g, tg = 64, 256, 8, 4
+    say(f"deepseek_v2_fp8_moe full router t={t} n_routed={n_routed}")
+    rng = np.random.default_rng(57)
+    x = (rng.integers(-16, 17, size=(t, D)) / 16.0).astype(np.float32)
+    wr = (rng.integers(-1, 2, size=(n_routed, D)) / 16.0).astype(np.float32)
+    bias = formats.round_to_bf16(rng.normal(scale=0.02, size=n_routed).astype(np.float32))
+    w1, s1, w2, s2 = _baseline_weights(n_routed + 1, seed=58)
+    xb = torch.from_numpy(x).to(DEV).to(torch.bfloat16)
+    out = aklr_amd.deepseek_v2_fp8_moe(xb, torch.from_numpy(wr).to(DEV).to(torch.bfloat16),
+                                       torch.from_numpy(bias).to(DEV).to(torch.bfloat16), w1, s1, w2, s2, TOPK, g, tg,
+                                       True, "sigmoid", 2.5)
+    assert isinstance(out, torch.Tensor), out
+    torch.cuda.synchronize()
+    logits = moe.router_logits(x, wr)
+    ids, wts = moe.grouped_topk(logits, bias, TOPK, g, tg, True, 2.5)
+    ids, wts = moe.with_shared_slot(ids, wts, n_routed)
+    assert len(np.unique(ids[:, :TOPK])) > 64, "the routing touches a small part of the experts"
+    toks = [0, 17, 38, 63]
+    ref = _sampled_reference(toks, xb, ids, wts, w1, s1, w2, s2)
+    q = moe.sqnr_db(formats.round_to_bf16(ref), f32(out[toks]))
     say(f"  sampled tokens sqnr {q:.1f} dB")
     assert q >= 30.0
 
