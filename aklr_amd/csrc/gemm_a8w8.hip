@@ -1111,6 +1111,24 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
       p.grid_x = (int)best_groups;
     }
   }
+  // Short K (<= 16 K blocks) at 4 or 8 row tiles, where 32-column workgroups make 192-256 of them: two
+  // compute waves, one K split, a 4-deep weight ring. No partials and no split-K epilogue; each
+  // workgroup re-reads A from L2, which costs less here than the partials. Measured on cold weights,
+  // 7168 x 2048, medians of interleaved runs (us, the plan above -> this one): m = 128 12.32 -> 10.76,
+  // m = 64 9.46 -> 7.57 (the same two waves with a 2-deep ring: 11.60 and 8.62; one split over 16- or
+  // 64-column workgroups: 12.11 / 7.88 and 12.01 / 8.62). On longer K (56-128 K blocks) every no-split
+  // plan lost by 35-80% (2112 x 7168 and 7168 x 16384 need the split to fill the chip).
+  if (fill && (p.mt == 4 || p.mt == 8) && KB <= 16) {
+    const int64_t groups = (n + 31) / 32;
+    if (groups >= 192 && groups <= 256) {
+      p.nw = 2;
+      p.nt = 1;
+      p.grid_x = (int)groups;
+      finish_splits(p, KB, 1);
+      p.dd = 4;
+      return p;
+    }
+  }
   // Long K at 7 waves of 4 or 8 row tiles: a deeper weight ring, 4 or 3 blocks (measured on cold weights,
   // 7168 x 16384, medians of interleaved runs, us: m = 64 26.26 -> 25.94, m = 128 33.50 -> 33.26; on
   // K <= 56 blocks the deeper rings were even or slower).
@@ -1167,12 +1185,12 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   } else if (d.mt == 1) d.nt == 2 ? launch_stream<1, 2, FMT, PRE>(a, d, s) : launch_stream<1, 1, FMT, PRE>(a, d, s);
   else if (d.mt == 2) d.nt == 2 ? launch_stream<2, 2, FMT, PRE>(a, d, s) : launch_stream<2, 1, FMT, PRE>(a, d, s);
   else if (d.mt == 4) {
-    if (d.nw == 2) launch_stream<4, 1, FMT, PRE, false, 1, 2>(a, d, s);
+    if (d.nw == 2) d.dd ? launch_stream<4, 1, FMT, PRE, false, 1, 2, 4, 4>(a, d, s) : launch_stream<4, 1, FMT, PRE, false, 1, 2>(a, d, s);
     else if (d.nw == 6) launch_stream<4, 1, FMT, PRE, false, 1, 6>(a, d, s);
     else if (d.nw == 7) d.dd ? launch_stream<4, 1, FMT, PRE, false, 1, 7, 4, 4>(a, d, s) : launch_stream<4, 1, FMT, PRE, false, 1, 7>(a, d, s);
     else d.nt == 2 ? launch_stream<4, 2, FMT, PRE>(a, d, s) : launch_stream<4, 1, FMT, PRE>(a, d, s);
   } else {
-    if (d.nw == 2) launch_stream<8, 1, FMT, PRE, false, 1, 2>(a, d, s);
+    if (d.nw == 2) d.dd ? launch_stream<8, 1, FMT, PRE, false, 1, 2, 4, 4>(a, d, s) : launch_stream<8, 1, FMT, PRE, false, 1, 2>(a, d, s);
     else if (d.nw == 6) launch_stream<8, 1, FMT, PRE, false, 1, 6>(a, d, s);
     else if (d.nw == 7) d.dd ? launch_stream<8, 1, FMT, PRE, false, 1, 7, 4, 3>(a, d, s) : launch_stream<8, 1, FMT, PRE, false, 1, 7>(a, d, s);
     else d.nt == 2 ? launch_stream<8, 2, FMT, PRE>(a, d, s) : launch_stream<8, 1, FMT, PRE>(a, d, s);

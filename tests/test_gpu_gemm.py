@@ -231,10 +231,13 @@ def test_small_and_ragged(m, n, k):
 
 # Stream-kernel edges (m <= 128): column groups past n (n not a multiple of the group's 64 or 128
 # columns, whole waves past n), one K block, padded row tiles (m = 96 runs 8 row tiles), bias on both
-# store paths (one and two column tiles per wave), and K splits with a ragged last split.
+# store paths (one and two column tiles per wave), and K splits with a ragged last split. The short-K
+# plan of two waves and one split at 4 and 8 row tiles: 7168 x 2048 at m = 96, a ragged last 32-column
+# group (6160 columns, 193 groups) with padded rows, and 256 groups at m = 50.
 @pytest.mark.parametrize("m,n,k,bias", [(20, 16, 640, True), (90, 4112, 1024, True), (96, 7168, 2048, False),
                                         (128, 4096, 128, True), (33, 48, 128, False), (120, 2112, 7168, True),
-                                        (65, 6144, 2304, False), (3, 4112, 1024, True), (16, 48, 384, False)])
+                                        (65, 6144, 2304, False), (3, 4112, 1024, True), (16, 48, 384, False),
+                                        (100, 6160, 1024, True), (50, 8192, 2048, False)])
 def test_stream_shapes(m, n, k, bias):
     _run_and_check(m, n, k, bias=bias, seed=51)
     _run_and_check(m, n, k, variant="b_shuffled", bias=False, seed=52)
