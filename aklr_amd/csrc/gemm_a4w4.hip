@@ -854,7 +854,10 @@ static Skinny4Plan plan_skinny4(int64_t m, int64_t n, int64_t k) {
   Skinny4Plan p;
   p.mt = m <= 16 ? 1 : 2;
   const int64_t KS = (k + 127) / 128;
-  p.nt = 2;
+  // one column tile per workgroup (twice the workgroups) on long K at one row tile: measured on cold
+  // weights at m = 1, 8192 x 28672 (224 K steps), 24.82 -> 22.83 us; on 8192-long K it was within 3% either
+  // way (10240 x 8192 11.44 -> 11.12 us, 57344 x 8192 42.84 -> 45.23) and keeps two
+  p.nt = (p.mt == 1 && KS >= 128) ? 1 : 2;
   p.groups = (int)((n + 16 * p.nt - 1) / (16 * p.nt));
   p.nw = 4;
   p.d = (p.mt == 1 && KS >= 128) ? 4 : 2;
@@ -865,17 +868,17 @@ static Skinny4Plan plan_skinny4(int64_t m, int64_t n, int64_t k) {
   return p;
 }
 
-template <int MT, int D, bool PRE, bool SSHUF>
+template <int MT, int NT, int D, bool PRE, bool SSHUF>
 static void launch_skinny4(const Gemm4Args& g, const Skinny4Plan& p, hipStream_t s) {
-  hipLaunchKernelGGL((gemm4_skinny_kernel<MT, 2, 4, D, PRE, SSHUF>), dim3((unsigned)p.groups, (unsigned)p.splits),
+  hipLaunchKernelGGL((gemm4_skinny_kernel<MT, NT, 4, D, PRE, SSHUF>), dim3((unsigned)p.groups, (unsigned)p.splits),
                      dim3(256), 0, s, g);
 }
 
 template <bool PRE, bool SSHUF>
 static void launch_skinny4(const Gemm4Args& g, const Skinny4Plan& p, hipStream_t s) {
-  if (p.mt == 1 && p.d == 4) launch_skinny4<1, 4, PRE, SSHUF>(g, p, s);
-  else if (p.mt == 1) launch_skinny4<1, 2, PRE, SSHUF>(g, p, s);
-  else launch_skinny4<2, 2, PRE, SSHUF>(g, p, s);
+  if (p.mt == 1 && p.d == 4) p.nt == 1 ? launch_skinny4<1, 1, 4, PRE, SSHUF>(g, p, s) : launch_skinny4<1, 2, 4, PRE, SSHUF>(g, p, s);
+  else if (p.mt == 1) launch_skinny4<1, 2, 2, PRE, SSHUF>(g, p, s);
+  else launch_skinny4<2, 2, 2, PRE, SSHUF>(g, p, s);
 }
 
 // Stream plan for 16 < m <= 32 (two row tiles; measured on MI355X over the Llama-70B MXFP4 shapes,
