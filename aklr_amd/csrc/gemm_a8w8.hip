@@ -523,9 +523,10 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
 }
 
 // ---------------------------------------------------------------------------------------------
-// lds (m > 128): TM x TN workgroup tiles, 8 waves in 2 (m) x 4 (n) -- 4 x 2 for TN = 224 -- each wave
-// (TM/WM) x (TN/WN), K steps of 128 through LDS rings of SA stages of A (with the step's a_scale column
-// and b_scale row) and SB stages of B, filled by direct-to-LDS buffer loads (no register staging): A runs
+// lds (m > 128): TM x TN workgroup tiles (TM = 64 only with TN = 128), 8 waves in 2 (m) x 4 (n) -- 4 x 2
+// for TN = 224 -- each wave (TM/WM) x (TN/WN), K steps of 128 through LDS rings of SA stages of A (with
+// the step's a_scale column and b_scale row) and SB stages of B, filled by direct-to-LDS buffer loads (no
+// register staging): A runs
 // SA - 1 stages ahead of the compute and B SB - 1. With SA = SB + 1, A -- the operand whose lines miss
 // L2 more often in the XCD tile order below (each A row block serves 4 resident tiles of an XCD, each B
 // column block 8) -- gets one stage more latency to hide than B in the same LDS. Every wave issues the
@@ -972,7 +973,19 @@ static double lds_cost(const Plan8& p, int64_t k) {
   return t;
 }
 
+// At m <= 256 on short K (<= 16 K blocks) 64x128 tiles run when they make at most 256 workgroups (with
+// the K split plan8_lds gives them): 128-row tiles make too few workgroups there without a K split, and
+// the split's partials cost more than its 4-8 K steps gain (the cost model above prices that split
+// below what it measures at these sizes). Measured on cold b_shuffled operands (us, the cost model's
+// tile -> 64x128): 7168 x 2048 at m = 256 15.8 -> 13.0 and at m = 192 15.3 -> 12.9; 3072 x 1536 at
+// m = 256 12.3 -> 10.4 (2 K splits). Where they make more workgroups (24576 x 1536: 768), on longer K
+// (2112 x 7168, 4096 x 8192, 7168 x 16384 at m = 256) and at m = 384 and 512 they measured 10-150%
+// slower than the cost model's tile.
 static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
+  if (m <= 256 && k <= 16 * 128) {
+    const Plan8 p = plan8_lds(m, n, k, 64, 128);
+    if ((int64_t)p.grid_x * p.splits <= 256) return p;
+  }
   static const int kShapes[8][2] = {{256, 256}, {256, 224}, {256, 192}, {192, 192},
                                     {256, 128}, {128, 256}, {128, 192}, {128, 128}};
   Plan8 best = plan8_lds(m, n, k, 128, 128);
@@ -1260,6 +1273,8 @@ static void launch_lds(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
     else if (t.tn == 224) launch_lds_t<256, 224, FMT, PRE, 3, 2>(a, t, s);
     else if (t.tn == 192) launch_lds_t<256, 192, FMT, PRE, 3, 2>(a, t, s);
     else launch_lds_t<256, 128, FMT, PRE>(a, t, s);
+  } else if (t.tm == 64) {
+    launch_lds_t<64, 128, FMT, PRE>(a, t, s);
   } else {
     if (t.tn == 256) launch_lds_t<128, 256, FMT, PRE>(a, t, s);
     else if (t.tn == 192) launch_lds_t<128, 192, FMT, PRE>(a, t, s);

@@ -5,7 +5,8 @@ element, y the oracle's fp32 result (dequantize to fp32, then matmul); the contr
 ToleranceBound (atol 1e-2, rtol 1e-2 + bf16 unit roundoff) is checked too for FP8.
 Full outputs are compared up to decode sizes; prefill sizes compare a seeded sample of rows x columns
 (the oracle computes exactly those) plus size-independent properties (determinism, linearity in the
-scales).
+scales). test_gpu_full_outputs.py compares every output at prefill sizes, against a float32
+restatement on the GPU that is itself pinned to the oracle.
 """
 from __future__ import annotations
 
@@ -271,6 +272,24 @@ def test_192_row_tiles(m, n, k, bias, fp16):
     out_dtype = torch.float16 if fp16 else None
     _run_and_check(m, n, k, bias=bias, out_dtype=out_dtype, seed=65, rows=128, cols=512)
     _run_and_check(m, n, k, variant="b_shuffled", seed=66, rows=128, cols=512)
+
+
+# The 64x128 LDS tile (m <= 256 on K <= 16 blocks, at most 256 tiles), every output compared: one K split
+# (7168 x 2048 at m = 256 and 192), 3 and 4 K splits (130 x 3072 x 1536: a ragged last row tile of 2 rows;
+# 250 and 240 x 1024 x 2048), a ragged last column tile (n = 4112), bias, fp16 output and e5m2 (bias and
+# e5m2 on the row-major variant only, as its contract has them).
+@pytest.mark.parametrize("m,n,k,variant,bias,fp16,e5", [
+    (256, 7168, 2048, "row_major", False, False, False),
+    (192, 7168, 2048, "b_shuffled", False, True, False),
+    (256, 3072, 1536, "b_shuffled", False, True, False),
+    (130, 3072, 1536, "row_major", True, True, False),
+    (250, 1024, 2048, "b_shuffled", False, False, False),
+    (240, 1024, 2048, "row_major", True, False, True),
+    (200, 4112, 256, "row_major", True, False, False),
+])
+def test_64_row_tiles(m, n, k, variant, bias, fp16, e5):
+    _run_and_check(m, n, k, variant=variant, bias=bias, out_dtype=torch.float16 if fp16 else None, seed=m + 700,
+                   dtype=torch.float8_e5m2 if e5 else torch.float8_e4m3fn, rows=m, cols=n)
 
 
 # The long-K plan (one row tile, >= 96 K blocks, 192-256 workgroups of 32 columns, one K split, each
