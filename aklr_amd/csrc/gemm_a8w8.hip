@@ -85,6 +85,10 @@ struct XStage {
 // holds one K block per group and the groups' partial sums meet in LDS at the end, in group order, so
 // a narrow workgroup covers its columns over the whole K range with no split-K partials in memory (the
 // plan then runs one K split).
+//
+// Row blocks: with gridDim.z > 1, workgroup (x, y, z) computes rows [z * MT * 16, + MT * 16) -- its A
+// rows, their a_scale and its output rows start there -- and its split-K arrival word and partials are
+// those of tile z * gridDim.x + x. (Not with fused quantization.)
 template <int MT, int NT, int NW, int D, int NS, int FMT, bool PRE, bool QA = false, int KW = 1, bool ROT = false>
 __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p) {
   static_assert(!QA || (MT == 1 && FMT == 0 && NW == 4 && KW == 1), "fused quantization: e4m3, one row tile, 4 waves");
@@ -105,6 +109,14 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   __shared__ f32x4 sRed[KW > 1 ? (NW - kWC) * MT * NT * 64 : 1];  // KW > 1: the groups' partial sums
   __shared__ unsigned arrive_slot;
 
+  if (!QA && blockIdx.z > 0) {
+    const int64_t m0 = (int64_t)blockIdx.z * MT * 16;
+    p.a += m0 * p.lda;
+    p.sa += m0 * p.sa_sm;
+    p.out = reinterpret_cast<uint16_t*>(p.out) + m0 * p.ldo;  // 16-bit outputs
+    p.m -= (int)m0;
+  }
+  const int tile = (int)(blockIdx.z * gridDim.x + blockIdx.x);  // the split-K word and partials' tile
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 15, g = lane >> 4;
@@ -136,14 +148,14 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int c0w = n0 + (w % kWC) * NT * 16;  // compute wave's first column
   const int col_w = c0w + 4 * g;     // + nt * 16: the lane's first output column
-  // split-K partials: one plane per split of gridDim.x * NW * MT * NT 1 KiB tiles (fp32 elements)
-  const int64_t stream_plane = (int64_t)gridDim.x * NW * MT * NT * 256;
-  const int64_t part_base = ((int64_t)blockIdx.x * NW + w) * (MT * NT) * 256 + lane * 4;
+  // split-K partials: one plane per split of gridDim.x * gridDim.z * NW * MT * NT 1 KiB tiles (fp32 elements)
+  const int64_t stream_plane = (int64_t)gridDim.x * gridDim.z * NW * MT * NT * 256;
+  const int64_t part_base = ((int64_t)tile * NW + w) * (MT * NT) * 256 + lane * 4;
 
   if (QA && w == NW) {
     // Fused quantization: the compute waves fill the A stages; the loader stages b_scale and keeps
     // the barrier count.
-    if (p.splits > 1) seen = splitk_peek(p.counters + blockIdx.x);
+    if (p.splits > 1) seen = splitk_peek(p.counters + tile);
     const int len = kb_end - kb_begin;
     const int last_row = (p.n - 1) >> 7;
     for (int i = lane; i < kNBlk * len; i += 64) {
@@ -155,7 +167,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   } else if (w == NW) {
     // Loader. Rows past m read the out-of-range offset: zeros, no memory access. The arrival word's
     // peek goes out first, so it has returned by the first full wait below.
-    if (p.splits > 1) seen = splitk_peek(p.counters + blockIdx.x);
+    if (p.splits > 1) seen = splitk_peek(p.counters + tile);
     const i32x4 ars = make_rsrc_words(p.a, rsrc_bytes((int64_t)(p.m - 1) * p.lda + p.k));
     const i32x4 sars =
         make_rsrc_words(p.sa, rsrc_bytes(((int64_t)(p.m - 1) * p.sa_sm + (int64_t)(KB - 1) * p.sa_sk + 1) * 4));
@@ -434,7 +446,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) store_partial4(prs, part_base + (mt * NT + nt) * 256, acc[mt][nt]);
     }
-    if (!splitk_arrive(p.counters + blockIdx.x, seen, p.splits, &arrive_slot, kArriver)) return;
+    if (!splitk_arrive(p.counters + tile, seen, p.splits, &arrive_slot, kArriver)) return;
     if (w >= kWC) return;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -913,11 +925,12 @@ struct Plan8 {
   int splits, kb_per_split;
   bool rot = false;  // stream: the long-K plan (each workgroup walks its K range from its own block)
   int dd = 0;        // stream: weight-ring depth when not the default (4 at 1-2 row tiles, 2 beyond)
+  int rt = 1;        // stream: row blocks of mt * 16 rows (grid z)
 };
 
 static void finish_splits(Plan8& p, int64_t KB, int64_t s) {
   // one arrival word per output tile must fit the region, and the count field the splits
-  if (s < 1 || p.grid_x > kSplitkMaxTiles) s = 1;
+  if (s < 1 || (int64_t)p.grid_x * p.rt > kSplitkMaxTiles) s = 1;
   if (s > kSplitkMaxSplits) s = kSplitkMaxSplits;
   p.kb_per_split = (int)((KB + s - 1) / s);
   p.splits = (int)((KB + p.kb_per_split - 1) / p.kb_per_split);
@@ -1010,11 +1023,44 @@ static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
 // workgroups of columns: the narrower workgroups then need fewer K splits, so less partial traffic,
 // for the same workgroup count), and K split in up to 4 parts until about 256 workgroups run (each
 // split >= 4 K blocks).
-static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
+static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool pre, bool fill = true) {
   Plan8 p;
   p.kind = Kernel8::kStream;
   p.tm = p.tn = 0;
   const int64_t KB = k / 128;
+  // Row blocks at m = 65..128 on K <= 64 blocks (preshuffled weights; row-major ones at <= 16): 64-row
+  // blocks (4 row tiles, grid z) of 64-column workgroups (4 compute waves, a 4-deep weight ring; 32
+  // columns and 2 waves on K <= 16 where that still makes <= 256 workgroups), K split in 2, 4, ... while
+  // the workgroups stay <= 256 and each split >= 8 K blocks. A workgroup then reads 64 rows of A and 64
+  // columns of the weight over its K range where the 8-row-tile plans read all 128 rows of A for 32-112
+  // columns. Measured on cold preshuffled weights at m = 128 (us, the 8-row-tile plan -> this one):
+  // 7168 x 2048 10.60 -> 7.98, 4096 x 8192 18.55 -> 16.13, 4096 x 4096 13.67 -> 10.83, 8192 x 1024
+  // 7.71 -> 5.93, 3072 x 1536 10.95 -> 6.07, 2112 x 7168 16.28 -> 15.23; m = 96 on 7168 x 2048 9.95 -> 7.78.
+  // Row-major weights (each 128-byte weight line read by two loads) gained on 7168 x 2048 (12.73 ->
+  // 10.92) and lost on 4096 x 8192 (21.67 -> 24.77). Where the workgroups would exceed 256 (24576 x
+  // 1536: 768) and on longer K (7168 x 16384: 34.0 -> 40.7) the 8-row-tile plans stay.
+  if (fill && m > 64 && m <= 128 && KB <= (pre ? 64 : 16)) {
+    const int64_t rt = (m + 63) / 64;
+    int nw = 4;
+    int64_t groups = (n + 63) / 64;
+    if (KB <= 16 && (n + 31) / 32 * rt <= 256) {
+      nw = 2;
+      groups = (n + 31) / 32;
+    }
+    if (groups * rt <= 256) {
+      int64_t s = 1;
+      while (s * 2 * groups * rt <= 256 && s * 2 * 8 <= KB) s *= 2;
+      p.mt = 4;
+      p.nt = 1;
+      p.nw = nw;
+      p.kw = 1;
+      p.rt = (int)rt;
+      p.grid_x = (int)groups;
+      p.dd = 4;
+      finish_splits(p, KB, s);
+      return p;
+    }
+  }
   p.mt = m <= 16 ? 1 : (m <= 32 ? 2 : (m <= 64 ? 4 : 8));
   p.nt = n >= 4096 && (m > 16 || (n + 63) / 64 > 256) ? 2 : 1;
   // At 4 and 8 row tiles and K <= 64 blocks, one column tile per wave while that leaves <= 256 column
@@ -1150,8 +1196,9 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
 }
 
 // fill = false keeps the one-row-tile plans at 4 compute waves (the fused-quantization kernel's shape).
-static Plan8 plan8(int64_t m, int64_t n, int64_t k, bool fill = true) {
-  if (m <= kStreamMaxM) return plan8_stream(m, n, k, fill);
+// pre: the weight is preshuffled (the stream plans depend on its layout, the LDS plans do not).
+static Plan8 plan8(int64_t m, int64_t n, int64_t k, bool pre, bool fill = true) {
+  if (m <= kStreamMaxM) return plan8_stream(m, n, k, pre, fill);
   return plan8_lds_best(m, n, k);
 }
 
@@ -1166,9 +1213,14 @@ static bool lds_nt_out(int64_t ldo_bytes) { return ldo_bytes != 8192 && ldo_byte
 static size_t workspace8(const Plan8& p) {
   if (p.splits <= 1) return 0;
   if (p.kind == Kernel8::kStream)  // whole 16x16 tiles of every wave of every column group
-    return kSplitkCounterBytes + (size_t)p.splits * (size_t)p.grid_x * p.nw * p.mt * p.nt * 1024;
+    return kSplitkCounterBytes + (size_t)p.splits * (size_t)p.grid_x * p.rt * p.nw * p.mt * p.nt * 1024;
   // lds: whole workgroup tiles
   return kSplitkCounterBytes + (size_t)p.splits * (size_t)p.grid_x * p.tm * p.tn * sizeof(float);
+}
+// The workspace a call of either weight layout needs (the workspace queries take no layout).
+static size_t workspace8_any(int64_t m, int64_t n, int64_t k) {
+  const size_t a = workspace8(plan8(m, n, k, false)), b = workspace8(plan8(m, n, k, true));
+  return a > b ? a : b;
 }
 
 // Stream kernel: NW compute waves (4 but for the fill and long-K plans) and 4 A stages (8 for the
@@ -1179,7 +1231,7 @@ template <int MT, int NT, int FMT, bool PRE, bool QA = false, int KW = 1, int NW
 static void launch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   constexpr int D = DD ? DD : (MT <= 2 ? 4 : 2);
   hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, NW, D, NS, FMT, PRE, QA, KW, ROT>),
-                     dim3((unsigned)d.grid_x, (unsigned)d.splits), dim3((NW + 1) * 64), 0, s, a);
+                     dim3((unsigned)d.grid_x, (unsigned)d.splits, (unsigned)d.rt), dim3((NW + 1) * 64), 0, s, a);
 }
 
 template <int FMT, bool PRE>
@@ -1201,7 +1253,8 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
     if (d.nw == 2) d.dd ? launch_stream<4, 1, FMT, PRE, false, 1, 2, 4, 4>(a, d, s) : launch_stream<4, 1, FMT, PRE, false, 1, 2>(a, d, s);
     else if (d.nw == 6) launch_stream<4, 1, FMT, PRE, false, 1, 6>(a, d, s);
     else if (d.nw == 7) d.dd ? launch_stream<4, 1, FMT, PRE, false, 1, 7, 4, 4>(a, d, s) : launch_stream<4, 1, FMT, PRE, false, 1, 7>(a, d, s);
-    else d.nt == 2 ? launch_stream<4, 2, FMT, PRE>(a, d, s) : launch_stream<4, 1, FMT, PRE>(a, d, s);
+    else if (d.nt == 2) launch_stream<4, 2, FMT, PRE>(a, d, s);
+    else d.dd ? launch_stream<4, 1, FMT, PRE, false, 1, 4, 4, 4>(a, d, s) : launch_stream<4, 1, FMT, PRE>(a, d, s);
   } else {
     if (d.nw == 2) d.dd ? launch_stream<8, 1, FMT, PRE, false, 1, 2, 4, 4>(a, d, s) : launch_stream<8, 1, FMT, PRE, false, 1, 2>(a, d, s);
     else if (d.nw == 6) launch_stream<8, 1, FMT, PRE, false, 1, 6>(a, d, s);
@@ -1217,10 +1270,11 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
 // The fused kernel runs the 4-wave plan (fill = false); it serves a call only where the GEMM's own plan
 // sums every output in the same order (the same K splits, no rotated K walk), so the fused call equals
 // the two ops bit for bit. Elsewhere the entry point runs the two kernels.
+// (At one row tile the plans do not depend on the weight layout.)
 static bool fused_quant_ok(int64_t m, int64_t n, int64_t k) {
-  const Plan8 f = plan8(m, n, k, false);
+  const Plan8 f = plan8(m, n, k, true, false);
   if (!(f.kind == Kernel8::kStream && f.mt == 1 && f.kw == 1 && f.nw == 4)) return false;
-  const Plan8 t = plan8(m, n, k);
+  const Plan8 t = plan8(m, n, k, true);
   return !t.rot && t.splits == f.splits;
 }
 
@@ -1235,11 +1289,11 @@ static void dispatch_stream_qa(const Gemm8Args& a, const Plan8& d, hipStream_t s
 // the same in every workspace.
 static size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
 static size_t quant_codes_offset(int64_t m, int64_t n, int64_t k) {  // past the GEMM's own workspace
-  const size_t gemm = up256(workspace8(plan8(m, n, k)));
+  const size_t gemm = up256(workspace8_any(m, n, k));
   return gemm > kSplitkCounterBytes ? gemm : kSplitkCounterBytes;
 }
 static size_t quant_gemm_workspace(int64_t m, int64_t n, int64_t k) {
-  if (fused_quant_ok(m, n, k)) return workspace8(plan8(m, n, k, false));
+  if (fused_quant_ok(m, n, k)) return workspace8(plan8(m, n, k, true, false));
   return quant_codes_offset(m, n, k) + up256((size_t)m * k) + up256((size_t)(k / 128) * m * 4);
 }
 
@@ -1288,7 +1342,7 @@ using namespace aklr;
 
 extern "C" size_t aklr_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k < 128) return 0;
-  return workspace8(plan8(m, n, k));
+  return workspace8_any(m, n, k);
 }
 
 // The FP8 GEMM with the scratch it needs taken from `workspace` (the caller's buffer of
@@ -1342,7 +1396,7 @@ int aklr::gemm8_entry(const void* a, int64_t lda, const void* b, int64_t ldb, co
   const bool pre = b_layout == AKLR_B_PRESHUFFLE_16x16;
   const bool e5 = fp8_dtype == AKLR_FP8_E5M2;
 
-  const Plan8 plan = plan8(m, n, k);
+  const Plan8 plan = plan8(m, n, k, pre);
   g.splits = plan.splits;
   g.kb_per_split = plan.kb_per_split;
   if (plan.splits > 1) {
@@ -1404,7 +1458,7 @@ extern "C" int aklr_quant_gemm_a8w8_blockscale(const void* x, int64_t ldx, const
   if (b_layout == AKLR_B_ROW_MAJOR && (ldb < k || ldb % 16 != 0 || ldb >= (1 << 23))) return AKLR_ERR_INVALID_ARGUMENT;
   if (ldbs < k / 128) return AKLR_ERR_INVALID_ARGUMENT;
   if (m == 0) return AKLR_OK;
-  const Plan8 plan = plan8(m, n, k, false);
+  const Plan8 plan = plan8(m, n, k, true, false);  // the fused kernel's plan (one row tile)
   const size_t need = quant_gemm_workspace(m, n, k);
   if (need > 0 && (!workspace || workspace_bytes < need || !aklr_aligned16(workspace))) return AKLR_ERR_WORKSPACE;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -1415,7 +1469,7 @@ extern "C" int aklr_quant_gemm_a8w8_blockscale(const void* x, int64_t ldx, const
     float* sc = reinterpret_cast<float*>(q + up256((size_t)m * k));
     int st = aklr_per_group_quant_fp8(x, ldx, q, sc, m, k, stream);
     if (st != AKLR_OK) return st;
-    const size_t gemm_ws = workspace8(plan8(m, n, k));
+    const size_t gemm_ws = workspace8_any(m, n, k);
     return aklr_gemm_a8w8_blockscale(q, k, b, ldb, sc, 1, m, b_scale, ldbs, bias, out, ldo, m, n, k,
                                      AKLR_FP8_E4M3FN, b_layout, out_dtype, gemm_ws ? ws : nullptr, gemm_ws, stream);
   }

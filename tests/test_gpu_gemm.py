@@ -292,6 +292,25 @@ def test_64_row_tiles(m, n, k, variant, bias, fp16, e5):
                    dtype=torch.float8_e5m2 if e5 else torch.float8_e4m3fn, rows=m, cols=n)
 
 
+# Stream plans with row blocks (m = 65..128 on K <= 64 blocks with preshuffled weights, <= 16 with row-major
+# ones): 64-row blocks over the grid's z, 64-column workgroups of 4 waves (32 columns and 2 waves at
+# 3072 x 1536), K split 1 or 2 ways; a second block of one row (m = 65), ragged n (4112: the last group
+# holds 16 columns), both layouts, bias and fp16 output, and row-major weights at 32 K blocks, which keep
+# the 8-row-tile plan. Every output compared.
+@pytest.mark.parametrize("m,n,k,variant,bias,fp16", [
+    (128, 7168, 2048, "b_shuffled", False, False),
+    (128, 7168, 2048, "row_major", True, True),
+    (65, 3072, 1536, "b_shuffled", False, True),
+    (100, 4096, 8192, "b_shuffled", False, False),
+    (128, 2112, 7168, "b_shuffled", False, False),
+    (96, 4112, 4096, "row_major", True, False),
+    (80, 4112, 1024, "row_major", False, True),
+])
+def test_row_block_plans(m, n, k, variant, bias, fp16):
+    _run_and_check(m, n, k, variant=variant, bias=bias, out_dtype=torch.float16 if fp16 else None, seed=m + 800,
+                   rows=m, cols=n)
+
+
 # The long-K plan (one row tile, >= 96 K blocks, 192-256 workgroups of 32 columns, one K split, each
 # workgroup starting its K walk at its own block): a ragged last workgroup (n = 6160: its second column
 # tile past n) at a K range that 193 workgroups do not divide, 256 workgroups at 100 K blocks, MN scales,

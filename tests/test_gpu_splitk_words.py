@@ -49,7 +49,8 @@ def _twice(call, need, what):
     assert torch.equal(out1.view(torch.int16), out2.view(torch.int16)), f"{what}: outputs differ"
 
 
-@pytest.mark.parametrize("m,n,k", [(16, 4096, 16384), (128, 2112, 7168), (256, 2112, 7168), (250, 1024, 2048)])
+@pytest.mark.parametrize("m,n,k", [(16, 4096, 16384), (128, 2112, 7168), (256, 2112, 7168), (250, 1024, 2048),
+                                   (100, 4096, 8192)])
 def test_fp8_split_words_reset(m, n, k):
     L = _lib.lib()
     need = L.aklr_gemm_a8w8_blockscale_workspace_bytes(m, n, k)
