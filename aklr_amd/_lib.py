@@ -25,6 +25,7 @@ SIGNATURES: dict[str, tuple] = {
     "aklr_per_group_quant_mxfp8": (_c_int, [_vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _vp]),
     "aklr_dynamic_mxfp4_quant": (_c_int, [_vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_int, _vp]),
     "aklr_gemm_a8w8_blockscale_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
+    "aklr_gemm_a8w8_blockscale_kernel": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
     "aklr_gemm_a8w8_blockscale": (
         _c_int,
         [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64,

@@ -911,7 +911,7 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
 // host-side planning
 
 // m <= kStreamMaxM streams the weight through the stream kernel (activations shared in LDS); larger m
-// runs the LDS kernel.
+// runs the LDS kernel, but for the row-block stream plans (plan8_rowblocks), which also take m = 129..256.
 static constexpr int64_t kStreamMaxM = 128;
 
 enum class Kernel8 { kStream, kLds };
@@ -989,11 +989,12 @@ static double lds_cost(const Plan8& p, int64_t k) {
 // At m <= 256 on short K (<= 16 K blocks) 64x128 tiles run when they make at most 256 workgroups (with
 // the K split plan8_lds gives them): 128-row tiles make too few workgroups there without a K split, and
 // the split's partials cost more than its 4-8 K steps gain (the cost model above prices that split
-// below what it measures at these sizes). Measured on cold b_shuffled operands (us, the cost model's
-// tile -> 64x128): 7168 x 2048 at m = 256 15.8 -> 13.0 and at m = 192 15.3 -> 12.9; 3072 x 1536 at
-// m = 256 12.3 -> 10.4 (2 K splits). Where they make more workgroups (24576 x 1536: 768), on longer K
-// (2112 x 7168, 4096 x 8192, 7168 x 16384 at m = 256) and at m = 384 and 512 they measured 10-150%
-// slower than the cost model's tile.
+// below what it measures at these sizes). Preshuffled weights take the row-block stream plans first
+// where those fit; the 64x128 tile serves row-major weights and the rest. Measured on cold operands
+// (us, the cost model's tile -> 64x128): 7168 x 2048 at m = 256 15.8 -> 13.0 and at m = 192 15.3 -> 12.9;
+// 3072 x 1536 at m = 256 12.3 -> 10.4 (2 K splits). Where they make more workgroups (24576 x 1536: 768),
+// on longer K (2112 x 7168, 4096 x 8192, 7168 x 16384 at m = 256) and at m = 384 and 512 they measured
+// 10-150% slower than the cost model's tile.
 static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
   if (m <= 256 && k <= 16 * 128) {
     const Plan8 p = plan8_lds(m, n, k, 64, 128);
@@ -1023,44 +1024,11 @@ static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
 // workgroups of columns: the narrower workgroups then need fewer K splits, so less partial traffic,
 // for the same workgroup count), and K split in up to 4 parts until about 256 workgroups run (each
 // split >= 4 K blocks).
-static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool pre, bool fill = true) {
+static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
   Plan8 p;
   p.kind = Kernel8::kStream;
   p.tm = p.tn = 0;
   const int64_t KB = k / 128;
-  // Row blocks at m = 65..128 on K <= 64 blocks (preshuffled weights; row-major ones at <= 16): 64-row
-  // blocks (4 row tiles, grid z) of 64-column workgroups (4 compute waves, a 4-deep weight ring; 32
-  // columns and 2 waves on K <= 16 where that still makes <= 256 workgroups), K split in 2, 4, ... while
-  // the workgroups stay <= 256 and each split >= 8 K blocks. A workgroup then reads 64 rows of A and 64
-  // columns of the weight over its K range where the 8-row-tile plans read all 128 rows of A for 32-112
-  // columns. Measured on cold preshuffled weights at m = 128 (us, the 8-row-tile plan -> this one):
-  // 7168 x 2048 10.60 -> 7.98, 4096 x 8192 18.55 -> 16.13, 4096 x 4096 13.67 -> 10.83, 8192 x 1024
-  // 7.71 -> 5.93, 3072 x 1536 10.95 -> 6.07, 2112 x 7168 16.28 -> 15.23; m = 96 on 7168 x 2048 9.95 -> 7.78.
-  // Row-major weights (each 128-byte weight line read by two loads) gained on 7168 x 2048 (12.73 ->
-  // 10.92) and lost on 4096 x 8192 (21.67 -> 24.77). Where the workgroups would exceed 256 (24576 x
-  // 1536: 768) and on longer K (7168 x 16384: 34.0 -> 40.7) the 8-row-tile plans stay.
-  if (fill && m > 64 && m <= 128 && KB <= (pre ? 64 : 16)) {
-    const int64_t rt = (m + 63) / 64;
-    int nw = 4;
-    int64_t groups = (n + 63) / 64;
-    if (KB <= 16 && (n + 31) / 32 * rt <= 256) {
-      nw = 2;
-      groups = (n + 31) / 32;
-    }
-    if (groups * rt <= 256) {
-      int64_t s = 1;
-      while (s * 2 * groups * rt <= 256 && s * 2 * 8 <= KB) s *= 2;
-      p.mt = 4;
-      p.nt = 1;
-      p.nw = nw;
-      p.kw = 1;
-      p.rt = (int)rt;
-      p.grid_x = (int)groups;
-      p.dd = 4;
-      finish_splits(p, KB, s);
-      return p;
-    }
-  }
   p.mt = m <= 16 ? 1 : (m <= 32 ? 2 : (m <= 64 ? 4 : 8));
   p.nt = n >= 4096 && (m > 16 || (n + 63) / 64 > 256) ? 2 : 1;
   // At 4 and 8 row tiles and K <= 64 blocks, one column tile per wave while that leaves <= 256 column
@@ -1196,9 +1164,53 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool pre, bool fill =
 }
 
 // fill = false keeps the one-row-tile plans at 4 compute waves (the fused-quantization kernel's shape).
-// pre: the weight is preshuffled (the stream plans depend on its layout, the LDS plans do not).
+// Row-block stream plans: 64-row blocks (4 row tiles) over the grid's z, so that a workgroup reads 64
+// rows of A and its own columns of the weight where the 8-row-tile plans read all 128 rows of A for
+// 32-112 columns and the LDS tiles split K. At m = 65..128 on K <= 64 blocks (row-major weights: <= 16)
+// with 2 (K <= 16 blocks) or 4 compute waves, at m = 129..256 on preshuffled weights and K <= 16 blocks
+// with 4 or 8: the narrowest workgroup (32, 64 or 128 columns) that makes at most 256 of them, and K
+// split 2, 4, ... ways while they stay <= 256 and each split keeps >= 8 K blocks. A 4-deep weight ring.
+// Measured on cold preshuffled weights (us, the plan before -> this one): m = 128: 7168 x 2048
+// 10.60 -> 7.98 (4 waves), 4096 x 8192 18.55 -> 16.13 (2 splits), 4096 x 4096 13.67 -> 10.83, 8192 x 1024
+// 7.71 -> 5.93, 3072 x 1536 10.95 -> 6.07 (2 waves), 2112 x 7168 16.28 -> 15.23; m = 96 on 7168 x 2048
+// 9.95 -> 7.78; m = 256 (the LDS 64x128 tile before): 7168 x 2048 12.92 -> 10.13 (8 waves), 3072 x 1536
+// 10.35 -> 6.68, 8192 x 1024 8.96 -> 7.17; m = 192 on 7168 x 2048 12.82 -> 9.88. Row-major weights (each
+// 128-byte weight line read by two loads) gained at m = 128 on 7168 x 2048 (12.73 -> 10.92) and lost on
+// 4096 x 8192 (21.67 -> 24.77) and at m = 256 (12.10 -> 15.63). Longer K at m > 128 (2112 x 7168:
+// 19.13 -> 21.45), more than 256 workgroups (24576 x 1536 at m = 128) and K > 64 blocks (7168 x 16384 at
+// m = 128: 34.0 -> 40.7) keep the other plans.
+static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p) {
+  const int64_t KB = k / 128;
+  if (m <= 64 || m > 256) return false;
+  if (m > 128 ? !(pre && KB <= 16) : KB > (pre ? 64 : 16)) return false;
+  const int64_t rt = (m + 63) / 64;
+  static const int kWaves[2][2] = {{2, 4}, {4, 8}};
+  for (const int nw : kWaves[m > 128]) {
+    if (nw == 2 && KB > 16) continue;
+    const int64_t groups = (n + nw * 16 - 1) / (nw * 16);
+    if (groups * rt > 256) continue;
+    int64_t s = 1;
+    while (s * 2 * groups * rt <= 256 && s * 2 * 8 <= KB) s *= 2;
+    p = Plan8{};
+    p.kind = Kernel8::kStream;
+    p.mt = 4;
+    p.nt = 1;
+    p.nw = nw;
+    p.kw = 1;
+    p.rt = (int)rt;
+    p.grid_x = (int)groups;
+    p.dd = 4;
+    finish_splits(p, KB, s);
+    return true;
+  }
+  return false;
+}
+
+// pre: the weight is preshuffled (the row-block plans depend on its layout).
 static Plan8 plan8(int64_t m, int64_t n, int64_t k, bool pre, bool fill = true) {
-  if (m <= kStreamMaxM) return plan8_stream(m, n, k, pre, fill);
+  Plan8 p;
+  if (fill && plan8_rowblocks(m, n, k, pre, p)) return p;
+  if (m <= kStreamMaxM) return plan8_stream(m, n, k, fill);
   return plan8_lds_best(m, n, k);
 }
 
@@ -1253,6 +1265,7 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
     if (d.nw == 2) d.dd ? launch_stream<4, 1, FMT, PRE, false, 1, 2, 4, 4>(a, d, s) : launch_stream<4, 1, FMT, PRE, false, 1, 2>(a, d, s);
     else if (d.nw == 6) launch_stream<4, 1, FMT, PRE, false, 1, 6>(a, d, s);
     else if (d.nw == 7) d.dd ? launch_stream<4, 1, FMT, PRE, false, 1, 7, 4, 4>(a, d, s) : launch_stream<4, 1, FMT, PRE, false, 1, 7>(a, d, s);
+    else if (d.nw == 8) launch_stream<4, 1, FMT, PRE, false, 1, 8, 4, 4>(a, d, s);
     else if (d.nt == 2) launch_stream<4, 2, FMT, PRE>(a, d, s);
     else d.dd ? launch_stream<4, 1, FMT, PRE, false, 1, 4, 4, 4>(a, d, s) : launch_stream<4, 1, FMT, PRE>(a, d, s);
   } else {
@@ -1434,6 +1447,12 @@ extern "C" int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void*
 extern "C" size_t aklr_quant_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k < 128) return 0;
   return quant_gemm_workspace(m, n, k);
+}
+
+extern "C" int aklr_gemm_a8w8_blockscale_kernel(int64_t m, int64_t n, int64_t k, int b_layout) {
+  if (m <= 0 || n <= 0 || k < 128 || k % 128 != 0) return -1;
+  if (b_layout != AKLR_B_ROW_MAJOR && b_layout != AKLR_B_PRESHUFFLE_16x16) return -1;
+  return plan8(m, n, k, b_layout == AKLR_B_PRESHUFFLE_16x16).kind == Kernel8::kStream ? 0 : 1;
 }
 
 extern "C" int aklr_quant_gemm_a8w8_blockscale_fused(int64_t m, int64_t n, int64_t k) {

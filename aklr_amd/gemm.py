@@ -188,7 +188,7 @@ def gemm_a8w8_blockwise_scaled(
     if not _out_ok(out, m, n, dt, a.device, (a, b, a_scale, b_scale, bias)):
         return _OOC
     b_layout = _lib.B_ROW_MAJOR if variant == "row_major" else _lib.B_PRESHUFFLE_16x16
-    path = "stream" if m <= 128 else "lds"  # the library picks the same way (kStreamMaxM)
+    path = ("stream", "lds")[_lib.lib().aklr_gemm_a8w8_blockscale_kernel(m, n, k, b_layout)]  # as the library picks
     # trans_b = False (row_major only, by the check above): b is (k, n), as the reference's _weight
     # transposes it (aklr/ops/gemm/reference.py:32-37)
     ref = f"aklr_gemm_a8w8_blockscale:{path}" if trans_b else f"aklr_transpose_b8+aklr_gemm_a8w8_blockscale:{path}"
@@ -274,7 +274,7 @@ def quant_gemm_a8w8_blockwise_scaled(x, b, b_scale, bias=None, out_dtype=None, o
     if not _out_ok(out, m, n, dt, x.device, (x, b, b_scale, bias)):
         return _OOC
     fused = _lib.lib().aklr_quant_gemm_a8w8_blockscale_fused(m, n, k) == 1  # as the library picks
-    path = "stream_fused" if fused else ("stream" if m <= 128 else "lds")
+    path = "stream_fused" if fused else ("stream", "lds")[_lib.lib().aklr_gemm_a8w8_blockscale_kernel(m, n, k, b_layout)]
     return _QuantGemm8Plan(x, b, b_scale, bias, out, dt, m, n, k, b_layout, variant,
                            f"aklr_quant_gemm_a8w8_blockscale:{path}")
 

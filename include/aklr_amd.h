@@ -109,6 +109,11 @@ int aklr_dynamic_mxfp4_quant(const void* x, int64_t x_row_stride, uint8_t* quant
  * k % 128 == 0, n % 16 == 0. All pointers 16-byte aligned; lda, ldb, ldo multiples of 16 bytes.
  */
 size_t aklr_gemm_a8w8_blockscale_workspace_bytes(int64_t m, int64_t n, int64_t k);
+/* Which kernel aklr_gemm_a8w8_blockscale runs (m, n, k) on with weight layout b_layout: 0 the stream
+ * kernel (weights streamed into registers, activations through LDS), 1 the LDS-tiled kernel, -1 for
+ * invalid sizes (a query for callers that report which kernel serves a call; no counterpart in the
+ * reference). */
+int aklr_gemm_a8w8_blockscale_kernel(int64_t m, int64_t n, int64_t k, int b_layout);
 int aklr_gemm_a8w8_blockscale(const void* a, int64_t lda, const void* b, int64_t ldb, const float* a_scale,
                               int64_t sa_stride_m, int64_t sa_stride_k, const float* b_scale, int64_t ldbs,
                               const float* bias, void* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
