@@ -535,10 +535,10 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
 }
 
 // ---------------------------------------------------------------------------------------------
-// lds (m > 128): TM x TN workgroup tiles (TM = 64 only with TN = 128), 8 waves in 2 (m) x 4 (n) -- 4 x 2
-// for TN = 224 -- each wave (TM/WM) x (TN/WN), K steps of 128 through LDS rings of SA stages of A (with
-// the step's a_scale column and b_scale row) and SB stages of B, filled by direct-to-LDS buffer loads (no
-// register staging): A runs
+// lds (m > 128; row-major weights from m = 65): TM x TN workgroup tiles (TM = 64 with TN = 64 or 128), 8
+// waves in 2 (m) x 4 (n) -- 4 x 2 for TN = 224 -- each wave (TM/WM) x (TN/WN), K steps of 128 through LDS
+// rings of SA stages of A (with the step's a_scale column and b_scale row) and SB stages of B, filled by
+// direct-to-LDS buffer loads (no register staging): A runs
 // SA - 1 stages ahead of the compute and B SB - 1. With SA = SB + 1, A -- the operand whose lines miss
 // L2 more often in the XCD tile order below (each A row block serves 4 resident tiles of an XCD, each B
 // column block 8) -- gets one stage more latency to hide than B in the same LDS. Every wave issues the
@@ -561,7 +561,8 @@ __host__ __device__ constexpr int lds8_stage_b(int tn) { return tn * 128; }
 
 template <int TM, int TN, int SA, int SB, int FMT, bool PRE>
 __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
-  static_assert(TM % 64 == 0 && TM <= 256 && (TN == 128 || TN == 192 || TN == 224 || TN == 256), "tile shape");
+  static_assert(TM % 64 == 0 && TM <= 256 && (TN == 64 || TN == 128 || TN == 192 || TN == 224 || TN == 256),
+                "tile shape");
   static_assert(SB >= 2 && (SA == SB || SA == SB + 1), "stage counts");
   constexpr int WN = TN == 224 ? 2 : 4, WM = 8 / WN;  // waves along n and m
   constexpr int MT = TM / (16 * WM), NT = TN / (16 * WN);  // 16x16 tiles per wave along m and n
@@ -589,8 +590,8 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   // its FMAs read a result that is already complete and issue while the matrix core works on later
   // tiles; folding the newest result instead stalls every step on the MFMA latency (measured 8-10%
   // slower on 256x224 tiles, bitwise the same output).
-  constexpr int kLag = 3;
   constexpr int kT = MT * NT;
+  constexpr int kLag = kT > 3 ? 3 : kT - 1;  // (64x64 tiles: 2 MFMA tiles a wave)
   static_assert(kT > kLag, "fold lag");
   static_assert(kScaleWaves < 8, "a wave left for the b_scale row");
   __shared__ __attribute__((aligned(1024))) uint8_t sA[SA * kStageA];
@@ -1164,25 +1165,26 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
 }
 
 // fill = false keeps the one-row-tile plans at 4 compute waves (the fused-quantization kernel's shape).
-// Row-block stream plans: 64-row blocks (4 row tiles) over the grid's z, so that a workgroup reads 64
-// rows of A and its own columns of the weight where the 8-row-tile plans read all 128 rows of A for
-// 32-112 columns and the LDS tiles split K. At m = 65..128 on K <= 64 blocks (row-major weights: <= 16)
-// with 2 (K <= 16 blocks) or 4 compute waves, at m = 129..256 on preshuffled weights and K <= 16 blocks
-// with 4 or 8: the narrowest workgroup (32, 64 or 128 columns) that makes at most 256 of them, and K
+// Row-block stream plans (preshuffled weights): 64-row blocks (4 row tiles) over the grid's z, so that a
+// workgroup reads 64 rows of A and its own columns of the weight where the 8-row-tile plans read all
+// 128 rows of A for 32-112 columns and the LDS tiles split K. At m = 65..128 on K <= 64 blocks with 2
+// (K <= 16 blocks) or 4 compute waves, at m = 129..256 on K <= 16 blocks with 4 or 8: the narrowest
+// workgroup (32, 64 or 128 columns) that makes at most 256 of them, and K
 // split 2, 4, ... ways while they stay <= 256 and each split keeps >= 8 K blocks. A 4-deep weight ring.
 // Measured on cold preshuffled weights (us, the plan before -> this one): m = 128: 7168 x 2048
 // 10.60 -> 7.98 (4 waves), 4096 x 8192 18.55 -> 16.13 (2 splits), 4096 x 4096 13.67 -> 10.83, 8192 x 1024
 // 7.71 -> 5.93, 3072 x 1536 10.95 -> 6.07 (2 waves), 2112 x 7168 16.28 -> 15.23; m = 96 on 7168 x 2048
 // 9.95 -> 7.78; m = 256 (the LDS 64x128 tile before): 7168 x 2048 12.92 -> 10.13 (8 waves), 3072 x 1536
 // 10.35 -> 6.68, 8192 x 1024 8.96 -> 7.17; m = 192 on 7168 x 2048 12.82 -> 9.88. Row-major weights (each
-// 128-byte weight line read by two loads) gained at m = 128 on 7168 x 2048 (12.73 -> 10.92) and lost on
-// 4096 x 8192 (21.67 -> 24.77) and at m = 256 (12.10 -> 15.63). Longer K at m > 128 (2112 x 7168:
+// 128-byte weight line read by two loads) gained less at m = 128 on 7168 x 2048 (12.73 -> 10.92; the
+// 64x64 LDS tile, 9.37, serves them) and lost on 4096 x 8192 (21.67 -> 24.77) and at m = 256 (12.10 ->
+// 15.63). Longer K at m > 128 (2112 x 7168:
 // 19.13 -> 21.45), more than 256 workgroups (24576 x 1536 at m = 128) and K > 64 blocks (7168 x 16384 at
 // m = 128: 34.0 -> 40.7) keep the other plans.
 static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p) {
   const int64_t KB = k / 128;
-  if (m <= 64 || m > 256) return false;
-  if (m > 128 ? !(pre && KB <= 16) : KB > (pre ? 64 : 16)) return false;
+  if (!pre || m <= 64 || m > 256) return false;
+  if (KB > (m > 128 ? 16 : 64)) return false;
   const int64_t rt = (m + 63) / 64;
   static const int kWaves[2][2] = {{2, 4}, {4, 8}};
   for (const int nw : kWaves[m > 128]) {
@@ -1206,9 +1208,16 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
   return false;
 }
 
-// pre: the weight is preshuffled (the row-block plans depend on its layout).
+// Row-major weights at m = 65..128 on K <= 16 blocks run 64x64 LDS tiles (4 stages; the K split of
+// plan8_lds): A and B both through whole-line loads into LDS, where the stream kernel reads each 128-byte
+// weight line with two loads. Measured on cold operands (us, the row-block stream plan -> 64x64):
+// 7168 x 2048 at m = 128 10.97 -> 9.37 (3, 6 and 8 stages: 10.03, 9.59, 9.84) and at m = 96 10.40 ->
+// 8.72. Preshuffled weights lost there (7.96 -> 9.44), and at m = 256 both layouts (row-major 12.05 ->
+// 14.00 against the 64x128 tile).
+// pre: the weight is preshuffled.
 static Plan8 plan8(int64_t m, int64_t n, int64_t k, bool pre, bool fill = true) {
   Plan8 p;
+  if (!pre && m > 64 && m <= 128 && k <= 16 * 128) return plan8_lds(m, n, k, 64, 64);
   if (fill && plan8_rowblocks(m, n, k, pre, p)) return p;
   if (m <= kStreamMaxM) return plan8_stream(m, n, k, fill);
   return plan8_lds_best(m, n, k);
@@ -1341,7 +1350,7 @@ static void launch_lds(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
     else if (t.tn == 192) launch_lds_t<256, 192, FMT, PRE, 3, 2>(a, t, s);
     else launch_lds_t<256, 128, FMT, PRE>(a, t, s);
   } else if (t.tm == 64) {
-    launch_lds_t<64, 128, FMT, PRE>(a, t, s);
+    t.tn == 64 ? launch_lds_t<64, 64, FMT, PRE>(a, t, s) : launch_lds_t<64, 128, FMT, PRE>(a, t, s);
   } else {
     if (t.tn == 256) launch_lds_t<128, 256, FMT, PRE>(a, t, s);
     else if (t.tn == 192) launch_lds_t<128, 192, FMT, PRE>(a, t, s);

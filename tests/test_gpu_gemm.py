@@ -274,10 +274,12 @@ def test_192_row_tiles(m, n, k, bias, fp16):
     _run_and_check(m, n, k, variant="b_shuffled", seed=66, rows=128, cols=512)
 
 
-# The 64x128 LDS tile (m <= 256 on K <= 16 blocks, at most 256 tiles; row-major weights, as preshuffled
-# ones take the row-block stream plans there), every output compared: one K split (7168 x 2048 at m = 256
-# and 192), 3 and 4 K splits (130 x 3072 x 1536: a ragged last row tile of 2 rows; 240 x 1024 x 2048), a
-# ragged last column tile (n = 4112), bias, fp16 output and e5m2.
+# The 64-row LDS tiles on row-major weights (preshuffled ones take the row-block stream plans there), every
+# output compared. 64x128 at m = 129..256 on K <= 16 blocks (at most 256 tiles): one K split (7168 x 2048
+# at m = 256 and 192), 3 and 4 K splits (130 x 3072 x 1536: a ragged last row tile of 2 rows;
+# 240 x 1024 x 2048), a ragged last column tile (n = 4112). 64x64 at m = 65..128 on K <= 16 blocks: one K
+# split (7168 x 2048 at m = 128 and 96), 2 K splits (100 x 3072 x 1536), a ragged last column tile of 16
+# (80 x 4112 x 1024). Bias, fp16 output and e5m2.
 @pytest.mark.parametrize("m,n,k,bias,fp16,e5", [
     (256, 7168, 2048, False, False, False),
     (192, 7168, 2048, False, True, False),
@@ -285,6 +287,10 @@ def test_192_row_tiles(m, n, k, bias, fp16):
     (130, 3072, 1536, True, True, False),
     (240, 1024, 2048, True, False, True),
     (200, 4112, 256, True, False, False),
+    (128, 7168, 2048, True, True, False),
+    (96, 7168, 2048, False, False, True),
+    (100, 3072, 1536, True, False, False),
+    (80, 4112, 1024, False, True, False),
 ])
 def test_64_row_tiles(m, n, k, bias, fp16, e5):
     assert aklr_amd._lib.lib().aklr_gemm_a8w8_blockscale_kernel(m, n, k, aklr_amd._lib.B_ROW_MAJOR) == 1
@@ -292,21 +298,19 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
                    dtype=torch.float8_e5m2 if e5 else torch.float8_e4m3fn, rows=m, cols=n)
 
 
-# Stream plans with row blocks: 64-row blocks over the grid's z (m = 65..128 on K <= 64 blocks with
-# preshuffled weights, <= 16 with row-major ones; m = 129..256 on preshuffled weights and K <= 16 blocks).
-# 64-column workgroups of 4 waves (32 columns and 2 waves at 3072 x 1536 and m <= 128; 128 columns and 8
-# waves at 7168 x 2048 and 8192 x 1024 past m = 128), K split 1 or 2 ways (2 at m = 250: 16 workgroups a
-# row block); a second block of one row (m = 65), a last block of 8 rows (m = 200), ragged n (4112: the
-# last group holds 16 columns), both layouts, bias and fp16 output, and row-major weights at 32 K blocks,
-# which keep the 8-row-tile plan. Every output compared.
+# Stream plans with row blocks (preshuffled weights): 64-row blocks over the grid's z (m = 65..128 on K <= 64
+# blocks; m = 129..256 on K <= 16 blocks). 64-column workgroups of 4 waves (32 columns and 2 waves at
+# 3072 x 1536 and m <= 128; 128 columns and 8 waves at 7168 x 2048 and 8192 x 1024 past m = 128), K split
+# 1 or 2 ways (2 at m = 250: 16 workgroups a row block); a second block of one row (m = 65), a last block
+# of 8 rows (m = 200), ragged n (4112: the last group holds 16 columns), fp16 output, and row-major
+# weights at 32 K blocks, which keep the 8-row-tile stream plan. Every output compared.
 @pytest.mark.parametrize("m,n,k,variant,bias,fp16,stream", [
     (128, 7168, 2048, "b_shuffled", False, False, True),
-    (128, 7168, 2048, "row_major", True, True, True),
     (65, 3072, 1536, "b_shuffled", False, True, True),
     (100, 4096, 8192, "b_shuffled", False, False, True),
     (128, 2112, 7168, "b_shuffled", False, False, True),
     (96, 4112, 4096, "row_major", True, False, True),
-    (80, 4112, 1024, "row_major", False, True, True),
+    (80, 4112, 4096, "b_shuffled", False, True, True),
     (256, 7168, 2048, "b_shuffled", False, False, True),
     (192, 7168, 2048, "b_shuffled", False, True, True),
     (200, 3072, 1536, "b_shuffled", False, False, True),
