@@ -842,6 +842,10 @@ def main(argv=None):
         cpu = cpu_baseline()
 
     traffic = load_traffic()
+    le16 = {}
+    for r in per_shape:
+        if r["m"] <= 16:
+            le16.setdefault(f"{r['n']}x{r['k']}", {})[f"m{r['m']}"] = round(r["gbs"] / HBM_PEAK_GBS, 3)
     line = {
         "metric": "block-scaled FP8 GEMM decode HBM GB/s (DeepSeek-V3 decode config)",
         "value": round(value, 1),
@@ -874,6 +878,8 @@ def main(argv=None):
             "traffic_source": (traffic or {}).get("source"),
             "launch_us": round(t_dom * 1e3, 2),
             "bytes_per_launch": dom_bytes,
+            # the north star's decode target (0.70 of HBM at M <= 16), per (N, K): each GEMM's fraction
+            "decode_m_le16_frac_hbm": le16,
         },
         "decode_per_shape": per_shape,
         **extras,
