@@ -182,6 +182,13 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t id, uint32_t total) {
   if (total < kXcd || (total % kXcd) != 0) return id;
   return (id % kXcd) * (total / kXcd) + id / kXcd;
 }
+// The same for any total: XCD x receives ids x, x + 8, ..., one more of them for x < total % 8, and its
+// logical ids are one consecutive range.
+__device__ __forceinline__ uint32_t xcd_remap_any(uint32_t id, uint32_t total) {
+  constexpr uint32_t kXcd = 8;
+  const uint32_t q = total / kXcd, r = total % kXcd, x = id % kXcd;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + id / kXcd;
+}
 
 // Two 16-byte halves -> one 32-byte MFMA operand (lo = bytes 0-15).
 __device__ __forceinline__ i32x8 cat(const u32x4& lo, const u32x4& hi) {

@@ -88,7 +88,17 @@ struct XStage {
 //
 // Row blocks: with gridDim.z > 1, workgroup (x, y, z) computes rows [z * MT * 16, + MT * 16) -- its A
 // rows, their a_scale and its output rows start there -- and its split-K arrival word and partials are
-// those of tile z * gridDim.x + x. (Not with fused quantization.)
+// those of tile z * gridDim.x + x. (Not with fused quantization.) With K splits, or where gridDim.x *
+// gridDim.y is not a multiple of 8, (x, y, z) come from a logical id, z fastest and then y, that keeps the
+// row blocks and K splits of a column group consecutive on one XCD, so they read its weight columns
+// through one L2: in hardware order the blocks of a column group are gridDim.x * gridDim.y ids apart and,
+// unless that is a multiple of 8, on different XCDs (M = 128, 2112 x 7168, 33 x 2 x 2 workgroups: 40.1 MB
+// fetched past L2 against 16.6 MB of operands). Interleaved A/B, cold weights, us (hardware order ->
+// logical): M = 128 on 2112 x 7168 15.21 -> 14.24, on 4096 x 8192 16.38 -> 15.99, M = 100 on 4096 x 8192
+// 15.67 -> 15.35. One split where that multiple of 8 already puts a group on one XCD keeps the hardware
+// order, which also spreads neighbouring groups over the 8 XCDs: the logical order measured 3-5% slower
+// there (M = 128 on 7168 x 2048 7.99 -> 8.32, on 3072 x 1536 6.08 -> 6.39; M = 256 on 8192 x 1024 7.18 ->
+// 7.54).
 template <int MT, int NT, int NW, int D, int NS, int FMT, bool PRE, bool QA = false, int KW = 1, bool ROT = false>
 __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p) {
   static_assert(!QA || (MT == 1 && FMT == 0 && NW == 4 && KW == 1), "fused quantization: e4m3, one row tile, 4 waves");
@@ -109,22 +119,30 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   __shared__ f32x4 sRed[KW > 1 ? (NW - kWC) * MT * NT * 64 : 1];  // KW > 1: the groups' partial sums
   __shared__ unsigned arrive_slot;
 
-  if (!QA && blockIdx.z > 0) {
-    const int64_t m0 = (int64_t)blockIdx.z * MT * 16;
+  uint32_t bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  if (!QA && gridDim.z > 1 && (gridDim.y > 1 || (gridDim.x * gridDim.y) % 8 != 0)) {
+    const uint32_t lid =
+        xcd_remap_any(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), gridDim.x * gridDim.y * gridDim.z);
+    bz = lid % gridDim.z;
+    by = (lid / gridDim.z) % gridDim.y;
+    bx = lid / (gridDim.z * gridDim.y);
+  }
+  if (!QA && bz > 0) {
+    const int64_t m0 = (int64_t)bz * MT * 16;
     p.a += m0 * p.lda;
     p.sa += m0 * p.sa_sm;
     p.out = reinterpret_cast<uint16_t*>(p.out) + m0 * p.ldo;  // 16-bit outputs
     p.m -= (int)m0;
   }
-  const int tile = (int)(blockIdx.z * gridDim.x + blockIdx.x);  // the split-K word and partials' tile
+  const int tile = (int)(bz * gridDim.x + bx);  // the split-K word and partials' tile
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * kCols;
+  const int n0 = (int)bx * kCols;
   // the loader's lane 0 arrives for the workgroup (split-K): it has no accumulators to keep in registers
   constexpr unsigned kArriver = NW * 64;
   uint64_t seen = 0;
-  const int split = blockIdx.y;
+  const int split = (int)by;
   const int KB = p.k >> 7;
   const int kb_begin = split * p.kb_per_split;
   const int kb_end = min(KB, kb_begin + p.kb_per_split);
@@ -133,7 +151,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   // ROT: workgroup x walks its K range from block r0 on, wrapping, so that at any moment the workgroups
   // fetch different A blocks and weight offsets (r0 spreads evenly over the grid).
   const int len_k = kb_end - kb_begin;
-  const int r0 = ROT ? (int)((int64_t)blockIdx.x * len_k / gridDim.x) : 0;
+  const int r0 = ROT ? (int)((int64_t)bx * len_k / gridDim.x) : 0;
   auto rotk = [&](int kb) {
     if constexpr (!ROT) return kb;
     const int t = kb - kb_begin + r0;
