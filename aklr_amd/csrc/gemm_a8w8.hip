@@ -621,8 +621,11 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   const int tiles_m = (p.m + TM - 1) / TM;
   const int tiles_n = (p.n + TN - 1) / TN;
   // XCD-aware order (the K splits of one tile are consecutive, so they share an XCD and its L2),
-  // then groups of kLdsGroup tile rows so neighbouring tiles share A rows and B columns.
-  const int lid = (int)xcd_remap(blockIdx.x, gridDim.x);
+  // then groups of kLdsGroup tile rows so neighbouring tiles share A rows and B columns. Workgroup
+  // counts that are not a multiple of 8 (the 192x192 tiles on N = 2112) get the same order (cold
+  // operands, us, hardware order -> this: 2112 x 7168 at m = 2048 50.3 -> 48.3, m = 4096 74.5 -> 73.5,
+  // m = 8192 144.1 -> 139.5).
+  const int lid = (int)xcd_remap_any(blockIdx.x, gridDim.x);
   const int pid = lid / p.splits, split = lid % p.splits;
   const int per_group = kLdsGroup * tiles_n;
   const int first_m = (pid / per_group) * kLdsGroup;
