@@ -1191,10 +1191,12 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
 // 128 rows of A for 32-112 columns and the LDS tiles split K. At m = 65..128 on K <= 64 blocks with 2
 // (K <= 16 blocks) or 4 compute waves, at m = 129..256 on K <= 16 blocks with 4 or 8: the narrowest
 // workgroup (32, 64 or 128 columns) that makes at most 256 of them, and K
-// split 2, 4, ... ways while they stay <= 256 and each split keeps >= 8 K blocks. A 4-deep weight ring.
+// split into as many parts as keep them <= 256 with >= 8 K blocks each. A 4-deep weight ring.
 // Measured on cold preshuffled weights (us, the plan before -> this one): m = 128: 7168 x 2048
 // 10.60 -> 7.98 (4 waves), 4096 x 8192 18.55 -> 16.13 (2 splits), 4096 x 4096 13.67 -> 10.83, 8192 x 1024
-// 7.71 -> 5.93, 3072 x 1536 10.95 -> 6.07 (2 waves), 2112 x 7168 16.28 -> 15.23; m = 96 on 7168 x 2048
+// 7.71 -> 5.93, 3072 x 1536 10.95 -> 6.07 (2 waves), 2112 x 7168 16.28 -> 12.25 (3 splits, 198 workgroups;
+// 2 splits 14.28), 576 x 7168 10.28 -> 9.71 (7 splits), 1536 x 7168 10.75 -> 10.87 (5 splits);
+// m = 96 on 512 x 7168 9.84 -> 9.53 (7 splits), on 7168 x 2048
 // 9.95 -> 7.78; m = 256 (the LDS 64x128 tile before): 7168 x 2048 12.92 -> 10.13 (8 waves), 3072 x 1536
 // 10.35 -> 6.68, 8192 x 1024 8.96 -> 7.17; m = 192 on 7168 x 2048 12.82 -> 9.88. Row-major weights (each
 // 128-byte weight line read by two loads) gained less at m = 128 on 7168 x 2048 (12.73 -> 10.92; the
@@ -1212,8 +1214,9 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
     if (nw == 2 && KB > 16) continue;
     const int64_t groups = (n + nw * 16 - 1) / (nw * 16);
     if (groups * rt > 256) continue;
-    int64_t s = 1;
-    while (s * 2 * groups * rt <= 256 && s * 2 * 8 <= KB) s *= 2;
+    int64_t s = 256 / (groups * rt);
+    if (s > KB / 8) s = KB / 8;
+    if (s < 1) s = 1;
     p = Plan8{};
     p.kind = Kernel8::kStream;
     p.mt = 4;
