@@ -1188,7 +1188,8 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
 // fill = false keeps the one-row-tile plans at 4 compute waves (the fused-quantization kernel's shape).
 // Row-block stream plans (preshuffled weights): 64-row blocks (4 row tiles) over the grid's z, so that a
 // workgroup reads 64 rows of A and its own columns of the weight where the 8-row-tile plans read all
-// 128 rows of A for 32-112 columns and the LDS tiles split K. At m = 65..128 on K <= 64 blocks with 2
+// 128 rows of A for 32-112 columns and the LDS tiles split K; 32-row blocks (2 row tiles) at m = 33..64,
+// where the 4-row-tile plan reads all 64 rows. At m = 33..128 on K <= 64 blocks with 2
 // (K <= 16 blocks) or 4 compute waves, at m = 129..256 on K <= 16 blocks with 4 or 8: the narrowest
 // workgroup (32, 64 or 128 columns) that makes at most 256 of them, and K
 // split into as many parts as keep them <= 256 with >= 8 K blocks each. A 4-deep weight ring.
@@ -1201,14 +1202,18 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
 // 10.35 -> 6.68, 8192 x 1024 8.96 -> 7.17; m = 192 on 7168 x 2048 12.82 -> 9.88. Row-major weights (each
 // 128-byte weight line read by two loads) gained less at m = 128 on 7168 x 2048 (12.73 -> 10.92; the
 // 64x64 LDS tile, 9.37, serves them) and lost on 4096 x 8192 (21.67 -> 24.77) and at m = 256 (12.10 ->
-// 15.63). Longer K at m > 128 (2112 x 7168:
-// 19.13 -> 21.45), more than 256 workgroups (24576 x 1536 at m = 128) and K > 64 blocks (7168 x 16384 at
-// m = 128: 34.0 -> 40.7) keep the other plans.
+// 15.63). At m = 64 (32-row blocks; the 4-row-tile plan before): 3072 x 1536 7.60 -> 4.93 (2 waves; 4
+// waves and 2 splits 6.89), 2112 x 7168 11.33 -> 10.24 (3 splits), 4096 x 4096 10.18 -> 9.21 (2 splits; 8
+// waves 9.86), 7168 x 2048 7.37 -> 6.79 (8 waves 9.30), 8192 x 1024 5.49 -> 5.07, 4096 x 8192 14.20 ->
+// 13.45; m = 48 on 7168 x 2048 7.04 -> 6.64. Longer K at m > 128 (2112 x 7168:
+// 19.13 -> 21.45), more than 256 workgroups (24576 x 1536 at m = 64 and 128; 8 waves there: 10.76 ->
+// 15.37 at m = 64) and K > 64 blocks (7168 x 16384 at m = 128: 34.0 -> 40.7) keep the other plans.
 static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p) {
   const int64_t KB = k / 128;
-  if (!pre || m <= 64 || m > 256) return false;
+  if (!pre || m <= 32 || m > 256) return false;
   if (KB > (m > 128 ? 16 : 64)) return false;
-  const int64_t rt = (m + 63) / 64;
+  const int mt = m <= 64 ? 2 : 4;  // 32-row blocks at m = 33..64, 64-row blocks above
+  const int64_t rt = (m + mt * 16 - 1) / (mt * 16);
   static const int kWaves[2][2] = {{2, 4}, {4, 8}};
   for (const int nw : kWaves[m > 128]) {
     if (nw == 2 && KB > 16) continue;
@@ -1219,7 +1224,7 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
     if (s < 1) s = 1;
     p = Plan8{};
     p.kind = Kernel8::kStream;
-    p.mt = 4;
+    p.mt = mt;
     p.nt = 1;
     p.nw = nw;
     p.kw = 1;
@@ -1293,7 +1298,11 @@ static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   } else if (d.mt == 1 && d.nw == 7) {
     launch_stream<1, 1, FMT, PRE, false, 1, 7>(a, d, s);
   } else if (d.mt == 1) d.nt == 2 ? launch_stream<1, 2, FMT, PRE>(a, d, s) : launch_stream<1, 1, FMT, PRE>(a, d, s);
-  else if (d.mt == 2) d.nt == 2 ? launch_stream<2, 2, FMT, PRE>(a, d, s) : launch_stream<2, 1, FMT, PRE>(a, d, s);
+  else if (d.mt == 2) {
+    if (d.nw == 2) launch_stream<2, 1, FMT, PRE, false, 1, 2, 4, 4>(a, d, s);  // row blocks
+    else if (d.dd) launch_stream<2, 1, FMT, PRE, false, 1, 4, 4, 4>(a, d, s);  // row blocks
+    else d.nt == 2 ? launch_stream<2, 2, FMT, PRE>(a, d, s) : launch_stream<2, 1, FMT, PRE>(a, d, s);
+  }
   else if (d.mt == 4) {
     if (d.nw == 2) d.dd ? launch_stream<4, 1, FMT, PRE, false, 1, 2, 4, 4>(a, d, s) : launch_stream<4, 1, FMT, PRE, false, 1, 2>(a, d, s);
     else if (d.nw == 6) launch_stream<4, 1, FMT, PRE, false, 1, 6>(a, d, s);

@@ -299,13 +299,14 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
 
 
 # Stream plans with row blocks (preshuffled weights): 64-row blocks over the grid's z (m = 65..128 on K <= 64
-# blocks; m = 129..256 on K <= 16 blocks). 64-column workgroups of 4 waves (32 columns and 2 waves at
-# 3072 x 1536 and m <= 128; 128 columns and 8 waves at 7168 x 2048 and 8192 x 1024 past m = 128), K split
-# into as many parts as keep <= 256 workgroups at >= 8 K blocks each (2 at m = 250: 16 workgroups a row
-# block; 3 at 2112 x 7168, the last holding 18 K blocks; 5 at 1536 x 7168, the last holding 8; 7 at
-# 576 x 7168); a second block of one row (m = 65), a last block
-# of 8 rows (m = 200), ragged n (4112: the last group holds 16 columns), fp16 output, and row-major
-# weights at 32 K blocks, which keep the 8-row-tile stream plan. Every output compared.
+# blocks; m = 129..256 on K <= 16 blocks), 32-row blocks at m = 33..64 on K <= 64 blocks. 64-column
+# workgroups of 4 waves (32 columns and 2 waves at 3072 x 1536 and m <= 128; 128 columns and 8 waves at
+# 7168 x 2048 and 8192 x 1024 past m = 128), K split into as many parts as keep <= 256 workgroups at >= 8
+# K blocks each (2 at m = 250: 16 workgroups a row block; 3 at 2112 x 7168, the last holding 18 K blocks;
+# 5 at 1536 x 7168, the last holding 8; 7 at 576 x 7168); a second block of one row (m = 65 and 33), a
+# last block of 8 rows (m = 200) and of 18 (m = 50), ragged n (4112: the last group holds 16 columns),
+# fp16 output, and row-major weights at 32 K blocks, which keep the 8-row-tile stream plan. Every output
+# compared.
 @pytest.mark.parametrize("m,n,k,variant,bias,fp16,stream", [
     (128, 7168, 2048, "b_shuffled", False, False, True),
     (65, 3072, 1536, "b_shuffled", False, True, True),
@@ -320,6 +321,12 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
     (200, 3072, 1536, "b_shuffled", False, False, True),
     (256, 8192, 1024, "b_shuffled", False, True, True),
     (250, 1024, 2048, "b_shuffled", False, False, True),
+    (64, 3072, 1536, "b_shuffled", False, False, True),
+    (33, 7168, 2048, "b_shuffled", False, True, True),
+    (64, 2112, 7168, "b_shuffled", False, False, True),
+    (50, 4112, 4096, "b_shuffled", False, False, True),
+    (64, 4096, 8192, "b_shuffled", False, True, True),
+    (48, 8192, 1024, "b_shuffled", False, False, True),
 ])
 def test_row_block_plans(m, n, k, variant, bias, fp16, stream):
     layout = aklr_amd._lib.B_ROW_MAJOR if variant == "row_major" else aklr_amd._lib.B_PRESHUFFLE_16x16
