@@ -1186,7 +1186,7 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
 }
 
 // fill = false keeps the one-row-tile plans at 4 compute waves (the fused-quantization kernel's shape).
-// Row-block stream plans (preshuffled weights): 64-row blocks (4 row tiles) over the grid's z, so that a
+// Row-block stream plans: 64-row blocks (4 row tiles) over the grid's z, so that a
 // workgroup reads 64 rows of A and its own columns of the weight where the 8-row-tile plans read all
 // 128 rows of A for 32-112 columns and the LDS tiles split K; 32-row blocks (2 row tiles) at m = 33..64,
 // where the 4-row-tile plan reads all 64 rows. At m = 33..128 on K <= 64 blocks with 2
@@ -1200,9 +1200,12 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
 // m = 96 on 512 x 7168 9.84 -> 9.53 (7 splits), on 7168 x 2048
 // 9.95 -> 7.78; m = 256 (the LDS 64x128 tile before): 7168 x 2048 12.92 -> 10.13 (8 waves), 3072 x 1536
 // 10.35 -> 6.68, 8192 x 1024 8.96 -> 7.17; m = 192 on 7168 x 2048 12.82 -> 9.88. Row-major weights (each
-// 128-byte weight line read by two loads) gained less at m = 128 on 7168 x 2048 (12.73 -> 10.92; the
-// 64x64 LDS tile, 9.37, serves them) and lost on 4096 x 8192 (21.67 -> 24.77) and at m = 256 (12.10 ->
-// 15.63). At m = 64 (32-row blocks; the 4-row-tile plan before): 3072 x 1536 7.60 -> 4.93 (2 waves; 4
+// 128-byte weight line read by two loads) take only the 2-wave plan (K <= 16 blocks, n <= 4096 at two
+// blocks): 3072 x 1536 8.27 -> 5.79 at m = 64 (the 4-row-tile plan before) and 7.73 -> 7.03 at m = 128 (the
+// 64x64 LDS tile before). With 4 or 8 waves they lost: at m = 128 on 7168 x 2048 9.34 (64x64 LDS tile)
+// -> 11.04, 4096 x 8192 21.55 -> 24.51, at m = 256 on 7168 x 2048 12.00 -> 15.58, at m = 64 on 7168 x 2048
+// 8.72 -> 9.24 and on 2112 x 7168 14.36 -> 14.57 (128 x 2112 x 7168 gained, 19.45 -> 17.85, and is left
+// to the 8-row-tile plan with the others). At m = 64 (32-row blocks; the 4-row-tile plan before): 3072 x 1536 7.60 -> 4.93 (2 waves; 4
 // waves and 2 splits 6.89), 2112 x 7168 11.33 -> 10.24 (3 splits), 4096 x 4096 10.18 -> 9.21 (2 splits; 8
 // waves 9.86), 7168 x 2048 7.37 -> 6.79 (8 waves 9.30), 8192 x 1024 5.49 -> 5.07, 4096 x 8192 14.20 ->
 // 13.45; m = 48 on 7168 x 2048 7.04 -> 6.64. Longer K at m > 128 (2112 x 7168:
@@ -1210,13 +1213,14 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
 // 15.37 at m = 64) and K > 64 blocks (7168 x 16384 at m = 128: 34.0 -> 40.7) keep the other plans.
 static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p) {
   const int64_t KB = k / 128;
-  if (!pre || m <= 32 || m > 256) return false;
+  if (m <= 32 || m > 256) return false;
   if (KB > (m > 128 ? 16 : 64)) return false;
   const int mt = m <= 64 ? 2 : 4;  // 32-row blocks at m = 33..64, 64-row blocks above
   const int64_t rt = (m + mt * 16 - 1) / (mt * 16);
   static const int kWaves[2][2] = {{2, 4}, {4, 8}};
   for (const int nw : kWaves[m > 128]) {
     if (nw == 2 && KB > 16) continue;
+    if (!pre && nw != 2) continue;  // row-major weights: the 2-wave plan only
     const int64_t groups = (n + nw * 16 - 1) / (nw * 16);
     if (groups * rt > 256) continue;
     int64_t s = 256 / (groups * rt);
@@ -1246,8 +1250,8 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
 // pre: the weight is preshuffled.
 static Plan8 plan8(int64_t m, int64_t n, int64_t k, bool pre, bool fill = true) {
   Plan8 p;
-  if (!pre && m > 64 && m <= 128 && k <= 16 * 128) return plan8_lds(m, n, k, 64, 64);
   if (fill && plan8_rowblocks(m, n, k, pre, p)) return p;
+  if (!pre && m > 64 && m <= 128 && k <= 16 * 128) return plan8_lds(m, n, k, 64, 64);
   if (m <= kStreamMaxM) return plan8_stream(m, n, k, fill);
   return plan8_lds_best(m, n, k);
 }

@@ -277,9 +277,9 @@ def test_192_row_tiles(m, n, k, bias, fp16):
 # The 64-row LDS tiles on row-major weights (preshuffled ones take the row-block stream plans there), every
 # output compared. 64x128 at m = 129..256 on K <= 16 blocks (at most 256 tiles): one K split (7168 x 2048
 # at m = 256 and 192), 3 and 4 K splits (130 x 3072 x 1536: a ragged last row tile of 2 rows;
-# 240 x 1024 x 2048), a ragged last column tile (n = 4112). 64x64 at m = 65..128 on K <= 16 blocks: one K
-# split (7168 x 2048 at m = 128 and 96), 2 K splits (100 x 3072 x 1536), a ragged last column tile of 16
-# (80 x 4112 x 1024). Bias, fp16 output and e5m2.
+# 240 x 1024 x 2048), a ragged last column tile (n = 4112). 64x64 at m = 65..128 on K <= 16 blocks, where
+# the 2-wave row blocks do not fit (n > 4096): 7168 x 2048 at m = 128 and 96, 7168 x 1536 with bias, a
+# ragged last column tile of 16 (80 x 4112 x 1024). Bias, fp16 output and e5m2.
 @pytest.mark.parametrize("m,n,k,bias,fp16,e5", [
     (256, 7168, 2048, False, False, False),
     (192, 7168, 2048, False, True, False),
@@ -289,7 +289,7 @@ def test_192_row_tiles(m, n, k, bias, fp16):
     (200, 4112, 256, True, False, False),
     (128, 7168, 2048, True, True, False),
     (96, 7168, 2048, False, False, True),
-    (100, 3072, 1536, True, False, False),
+    (100, 7168, 1536, True, False, False),
     (80, 4112, 1024, False, True, False),
 ])
 def test_64_row_tiles(m, n, k, bias, fp16, e5):
@@ -305,8 +305,9 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
 # K blocks each (2 at m = 250: 16 workgroups a row block; 3 at 2112 x 7168, the last holding 18 K blocks;
 # 5 at 1536 x 7168, the last holding 8; 7 at 576 x 7168); a second block of one row (m = 65 and 33), a
 # last block of 8 rows (m = 200) and of 18 (m = 50), ragged n (4112: the last group holds 16 columns),
-# fp16 output, and row-major weights at 32 K blocks, which keep the 8-row-tile stream plan. Every output
-# compared.
+# fp16 output, row-major weights on the 2-wave plan (3072 x 1536 at m = 64, 100 and 128, with bias; 2048 x
+# 2048 at m = 64 with 2 K splits), and
+# row-major weights at 32 K blocks, which keep the 8-row-tile stream plan. Every output compared.
 @pytest.mark.parametrize("m,n,k,variant,bias,fp16,stream", [
     (128, 7168, 2048, "b_shuffled", False, False, True),
     (65, 3072, 1536, "b_shuffled", False, True, True),
@@ -327,6 +328,10 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
     (50, 4112, 4096, "b_shuffled", False, False, True),
     (64, 4096, 8192, "b_shuffled", False, True, True),
     (48, 8192, 1024, "b_shuffled", False, False, True),
+    (64, 3072, 1536, "row_major", True, False, True),
+    (100, 3072, 1536, "row_major", False, True, True),
+    (128, 3072, 1536, "row_major", True, False, True),
+    (64, 2048, 2048, "row_major", False, False, True),
 ])
 def test_row_block_plans(m, n, k, variant, bias, fp16, stream):
     layout = aklr_amd._lib.B_ROW_MAJOR if variant == "row_major" else aklr_amd._lib.B_PRESHUFFLE_16x16
