@@ -985,8 +985,10 @@ static Plan8 plan8_lds(int64_t m, int64_t n, int64_t k, int tm, int tn, int64_t 
 // m = 128..8192 (it picks the fastest measured plan, or one within 2% of it, on all of them; and the
 // fastest, or within 4%, of sweeps with the 192- and 224-column tiles at m = 1024..8192): per K block
 // of one tile (256x256: 1.96, 256x224: 1.76, 256x192: 1.55, 192x192: 1.25, 256x128 and 128x256: 1.15,
-// 128x192: 0.90, 128x128: 0.70), rounds of 256 workgroups, a fixed 3 us per round, and for a K split the
-// partial traffic (s * tile * 4 bytes, stored and then summed by one workgroup at ~100 GB/s) plus 3 us.
+// 128x192: 0.90, 128x128: 0.70, 64x128: 0.58, 64x64: 0.35), rounds of 256 workgroups, a fixed 3 us per
+// round, and for a K split the partial traffic (s * tile * 4 bytes, stored and then summed by one
+// workgroup at ~100 GB/s) plus 3 us. (The 64-row figures are fits to sweeps of 64x64 and 64x128 tiles at
+// 1-4 K splits over 13 shapes with m = 256..2048, n = 512..8192 and K = 256..7168.)
 // The 192x192 tile serves N = 2112 = 11 x 192, where 22 x 11 = 242 tiles fill the chip at m = 4096 and
 // 256-row tiles leave 80 CUs idle (cold operands, us, 256x192 -> 192x192: m = 4096 93.5 -> 72.3,
 // m = 8192 158.0 -> 137.8; 128x192 -> 192x192 at m = 2048: 52.5 -> 48.9). On ten other reference and
@@ -999,7 +1001,9 @@ static double lds_cost(const Plan8& p, int64_t k) {
                       : area == 36864 ? 1.25
                       : area == 32768 ? 1.15
                       : area == 24576 ? 0.90
-                                      : 0.70;
+                      : area == 16384 ? 0.70
+                      : area == 8192  ? 0.58
+                                      : 0.35;
   const int64_t wgs = (int64_t)p.grid_x * p.splits;
   const double rounds = (double)((wgs + 255) / 256);
   double t = rounds * (p.kb_per_split * step + 3.0);
@@ -1017,23 +1021,32 @@ static double lds_cost(const Plan8& p, int64_t k) {
 // 3072 x 1536 at m = 256 12.3 -> 10.4 (2 K splits). Where they make more workgroups (24576 x 1536: 768),
 // on longer K (2112 x 7168, 4096 x 8192, 7168 x 16384 at m = 256) and at m = 384 and 512 they measured
 // 10-150% slower than the cost model's tile.
+// Past that, the cost model picks among the tiles below, each at the split count plan8_lds gives it and
+// unsplit. The 64-row tiles win where the output is small (at most 256 64x64 tiles, or 256 64x128
+// ones): cold preshuffled operands, us, the earlier pick (128-row tiles, split to fill the chip) -> this:
+// 256 x 512 x 4096 14.1 -> 8.9 (64x64, 4 splits), 512 x 1024 x 4096 15.0 -> 11.3 (64x64, 2), 1024 x 512
+// x 4096 14.9 -> 11.2, 256 x 4096 x 4096 16.9 -> 14.5 (64x64, none), 512 x 2048 x 4096 16.6 -> 14.2,
+// 512 x 4096 x 1024 13.7 -> 9.0 (64x128, none), 512 x 4096 x 2048 16.6 -> 13.0, 512 x 4096 x 256 6.7 ->
+// 5.8. The DeepSeek-V3 prefill shapes and the reference's other recorded shapes keep their tiles.
 static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
   if (m <= 256 && k <= 16 * 128) {
     const Plan8 p = plan8_lds(m, n, k, 64, 128);
     if ((int64_t)p.grid_x * p.splits <= 256) return p;
   }
-  static const int kShapes[8][2] = {{256, 256}, {256, 224}, {256, 192}, {192, 192},
-                                    {256, 128}, {128, 256}, {128, 192}, {128, 128}};
+  static const int kShapes[10][2] = {{256, 256}, {256, 224}, {256, 192}, {192, 192}, {256, 128},
+                                     {128, 256}, {128, 192}, {128, 128}, {64, 128},  {64, 64}};
   Plan8 best = plan8_lds(m, n, k, 128, 128);
   double best_t = lds_cost(best, k);
   for (const auto& sh : kShapes) {
     if (sh[0] > 128 && m <= 128) continue;  // half of every A tile would be padding
     if ((sh[1] == 192 || sh[1] == 224) && n % sh[1] != 0) continue;  // only where they fit N exactly
-    const Plan8 p = plan8_lds(m, n, k, sh[0], sh[1]);
-    const double t = lds_cost(p, k);
-    if (t < best_t) {
-      best = p;
-      best_t = t;
+    for (const int64_t s : {int64_t{0}, int64_t{1}}) {  // plan8_lds's split count, then none
+      const Plan8 p = plan8_lds(m, n, k, sh[0], sh[1], s);
+      const double t = lds_cost(p, k);
+      if (t < best_t) {
+        best = p;
+        best_t = t;
+      }
     }
   }
   return best;

@@ -340,6 +340,26 @@ def test_row_block_plans(m, n, k, variant, bias, fp16, stream):
                    rows=m, cols=n)
 
 
+# LDS plans of 64-row tiles past m = 256, where the output is small: 64x64 tiles at 4, 2 and 1 K splits
+# (256 x 512 x 4096, 512 x 1024 x 4096 / 1000 x 512 x 4096 / 777 x 1024 x 4096 and 384 x 2048 x 3072),
+# 64x128 unsplit (512 x 4096 x 1024; 300 x 4112 x 2048 with a ragged last row tile of 44 rows and a last
+# column tile of 16); both layouts, bias, fp16 and e5m2. Every output compared.
+@pytest.mark.parametrize("m,n,k,variant,bias,fp16,e5", [
+    (256, 512, 4096, "b_shuffled", False, False, False),
+    (512, 1024, 4096, "row_major", True, True, False),
+    (1000, 512, 4096, "b_shuffled", False, False, False),
+    (777, 1024, 4096, "row_major", False, False, True),
+    (384, 2048, 3072, "b_shuffled", False, True, False),
+    (512, 4096, 1024, "b_shuffled", False, False, False),
+    (300, 4112, 2048, "row_major", True, False, False),
+])
+def test_small_output_lds_plans(m, n, k, variant, bias, fp16, e5):
+    layout = aklr_amd._lib.B_ROW_MAJOR if variant == "row_major" else aklr_amd._lib.B_PRESHUFFLE_16x16
+    assert aklr_amd._lib.lib().aklr_gemm_a8w8_blockscale_kernel(m, n, k, layout) == 1
+    _run_and_check(m, n, k, variant=variant, bias=bias, out_dtype=torch.float16 if fp16 else None,
+                   dtype=torch.float8_e5m2 if e5 else torch.float8_e4m3fn, seed=m + 900, rows=m, cols=n)
+
+
 # The long-K plan (one row tile, >= 96 K blocks, 192-256 workgroups of 32 columns, one K split, each
 # workgroup starting its K walk at its own block): a ragged last workgroup (n = 6160: its second column
 # tile past n) at a K range that 193 workgroups do not divide, 256 workgroups at 100 K blocks, MN scales,
