@@ -1012,27 +1012,19 @@ static double lds_cost(const Plan8& p, int64_t k) {
   return t;
 }
 
-// At m <= 256 on short K (<= 16 K blocks) 64x128 tiles run when they make at most 256 workgroups (with
-// the K split plan8_lds gives them): 128-row tiles make too few workgroups there without a K split, and
-// the split's partials cost more than its 4-8 K steps gain (the cost model above prices that split
-// below what it measures at these sizes). Preshuffled weights take the row-block stream plans first
-// where those fit; the 64x128 tile serves row-major weights and the rest. Measured on cold operands
-// (us, the cost model's tile -> 64x128): 7168 x 2048 at m = 256 15.8 -> 13.0 and at m = 192 15.3 -> 12.9;
-// 3072 x 1536 at m = 256 12.3 -> 10.4 (2 K splits). Where they make more workgroups (24576 x 1536: 768),
-// on longer K (2112 x 7168, 4096 x 8192, 7168 x 16384 at m = 256) and at m = 384 and 512 they measured
-// 10-150% slower than the cost model's tile.
-// Past that, the cost model picks among the tiles below, each at the split count plan8_lds gives it and
-// unsplit. The 64-row tiles win where the output is small (at most 256 64x64 tiles, or 256 64x128
-// ones): cold preshuffled operands, us, the earlier pick (128-row tiles, split to fill the chip) -> this:
-// 256 x 512 x 4096 14.1 -> 8.9 (64x64, 4 splits), 512 x 1024 x 4096 15.0 -> 11.3 (64x64, 2), 1024 x 512
-// x 4096 14.9 -> 11.2, 256 x 4096 x 4096 16.9 -> 14.5 (64x64, none), 512 x 2048 x 4096 16.6 -> 14.2,
-// 512 x 4096 x 1024 13.7 -> 9.0 (64x128, none), 512 x 4096 x 2048 16.6 -> 13.0, 512 x 4096 x 256 6.7 ->
-// 5.8. The DeepSeek-V3 prefill shapes and the reference's other recorded shapes keep their tiles.
+// The cost model picks among the tiles below, each at the split count plan8_lds gives it and unsplit.
+// The 64-row tiles win where the output is small (at most 256 64x64 tiles, or 256 64x128 ones): there
+// the 128-row tiles, split to fill the chip, lost; their split costs more than the model priced. Cold
+// preshuffled operands, us, the earlier pick (128-row tiles) -> this: 256 x 512 x 4096 14.1 -> 8.9 (64x64,
+// 4 splits), 512 x 1024 x 4096 15.0 -> 11.3 (64x64, 2), 1024 x 512 x 4096 14.9 -> 11.2, 256 x 4096 x 4096
+// 16.9 -> 14.5 (64x64, none), 512 x 2048 x 4096 16.6 -> 14.2, 512 x 4096 x 1024 13.7 -> 9.0 (64x128, none),
+// 512 x 4096 x 2048 16.6 -> 13.0, 512 x 4096 x 256 6.7 -> 5.8. On short K (<= 16 K blocks) at m = 129..256
+// it gives 64x128 tiles on wide N (7168 x 2048 at m = 256 15.8 -> 13.0 and at m = 192 15.3 -> 12.9 against
+// the 128-row tiles it picked before) and unsplit 64x64 ones up to N = 4096 (row-major 3072 x 1536 at
+// m = 256 9.9 -> 7.4 and at m = 192 9.0 -> 7.4 against split 64x128 ones). Preshuffled weights take the
+// row-block stream plans first where those fit. The DeepSeek-V3 prefill shapes and the reference's other
+// recorded shapes keep their tiles.
 static Plan8 plan8_lds_best(int64_t m, int64_t n, int64_t k) {
-  if (m <= 256 && k <= 16 * 128) {
-    const Plan8 p = plan8_lds(m, n, k, 64, 128);
-    if ((int64_t)p.grid_x * p.splits <= 256) return p;
-  }
   static const int kShapes[10][2] = {{256, 256}, {256, 224}, {256, 192}, {192, 192}, {256, 128},
                                      {128, 256}, {128, 192}, {128, 128}, {64, 128},  {64, 64}};
   Plan8 best = plan8_lds(m, n, k, 128, 128);

@@ -275,11 +275,12 @@ def test_192_row_tiles(m, n, k, bias, fp16):
 
 
 # The 64-row LDS tiles on row-major weights (preshuffled ones take the row-block stream plans there), every
-# output compared. 64x128 at m = 129..256 on K <= 16 blocks (at most 256 tiles): one K split (7168 x 2048
-# at m = 256 and 192), 3 and 4 K splits (130 x 3072 x 1536: a ragged last row tile of 2 rows;
-# 240 x 1024 x 2048), a ragged last column tile (n = 4112). 64x64 at m = 65..128 on K <= 16 blocks, where
-# the 2-wave row blocks do not fit (n > 4096): 7168 x 2048 at m = 128 and 96, 7168 x 1536 with bias, a
-# ragged last column tile of 16 (80 x 4112 x 1024). Bias, fp16 output and e5m2.
+# output compared. At m = 129..256 on K <= 16 blocks: 64x128 on wide N (7168 x 2048 at m = 256 and 192; a
+# ragged last column tile of 16, 200 x 4112 x 256), unsplit 64x64 up to N = 4096 (256 x 3072 x 1536;
+# 130 x 3072 x 1536 with a ragged last row tile of 2 rows), 64x64 with 4 K splits (240 x 1024 x 2048).
+# 64x64 at m = 65..128 on K <= 16 blocks, where the 2-wave row blocks do not fit (n > 4096): 7168 x 2048 at
+# m = 128 and 96, 7168 x 1536 with bias, a ragged last column tile of 16 (80 x 4112 x 1024). Bias, fp16
+# output and e5m2.
 @pytest.mark.parametrize("m,n,k,bias,fp16,e5", [
     (256, 7168, 2048, False, False, False),
     (192, 7168, 2048, False, True, False),
@@ -340,10 +341,11 @@ def test_row_block_plans(m, n, k, variant, bias, fp16, stream):
                    rows=m, cols=n)
 
 
-# LDS plans of 64-row tiles past m = 256, where the output is small: 64x64 tiles at 4, 2 and 1 K splits
-# (256 x 512 x 4096, 512 x 1024 x 4096 / 1000 x 512 x 4096 / 777 x 1024 x 4096 and 384 x 2048 x 3072),
-# 64x128 unsplit (512 x 4096 x 1024; 300 x 4112 x 2048 with a ragged last row tile of 44 rows and a last
-# column tile of 16); both layouts, bias, fp16 and e5m2. Every output compared.
+# LDS plans of 64-row tiles where the output is small: 64x64 tiles at 4, 2 and 1 K splits (256 x 512 x
+# 4096, 512 x 1024 x 4096 / 1000 x 512 x 4096 / 777 x 1024 x 4096 and 384 x 2048 x 3072), 64x128 unsplit
+# (512 x 4096 x 1024; 300 x 4112 x 2048 with a ragged last row tile of 44 rows and a last column tile of
+# 16) and with 3 and 4 K splits (2112 x 7168 at m = 256, 200 and 192: last column tiles of 64, and at
+# m = 200 a last row tile of 8); both layouts, bias, fp16 and e5m2. Every output compared.
 @pytest.mark.parametrize("m,n,k,variant,bias,fp16,e5", [
     (256, 512, 4096, "b_shuffled", False, False, False),
     (512, 1024, 4096, "row_major", True, True, False),
@@ -352,6 +354,9 @@ def test_row_block_plans(m, n, k, variant, bias, fp16, stream):
     (384, 2048, 3072, "b_shuffled", False, True, False),
     (512, 4096, 1024, "b_shuffled", False, False, False),
     (300, 4112, 2048, "row_major", True, False, False),
+    (256, 2112, 7168, "b_shuffled", False, False, False),
+    (192, 2112, 7168, "b_shuffled", False, True, False),
+    (200, 2112, 7168, "row_major", True, False, False),
 ])
 def test_small_output_lds_plans(m, n, k, variant, bias, fp16, e5):
     layout = aklr_amd._lib.B_ROW_MAJOR if variant == "row_major" else aklr_amd._lib.B_PRESHUFFLE_16x16
