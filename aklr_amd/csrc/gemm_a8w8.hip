@@ -1219,6 +1219,34 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
 static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p) {
   const int64_t KB = k / 128;
   if (m <= 32 || m > 256) return false;
+  // m = 33..128 on 16..32 K blocks (preshuffled weights): 32-row blocks whose 4 waves split K among
+  // themselves (4 groups of one wave, 16 columns, while that makes <= 256 workgroups; else 2 groups of
+  // two, 32 columns, from 24 K blocks), no K split across workgroups, so no partials. Measured on cold
+  // weights, us (the row-block plan with K splits before -> this): m = 128: 512 x 4096 8.25 -> 6.35,
+  // 1024 x 4096 8.76 -> 6.56, 1024 x 2048 7.04 -> 5.23, 2048 x 4096 9.15 -> 7.42 (2 groups); m = 96: 512 x
+  // 4096 8.22 -> 6.42, 1536 x 4096 9.01 -> 7.27 (2); m = 64: 512 / 1024 / 1536 x 4096 6.80 / 7.36 / 7.61 ->
+  // 6.34 / 6.41 / 6.69, 4096 x 4096 9.19 -> 7.90 (2), 2048 x 2048 5.97 -> 5.21; m = 48: 2048 x 4096 7.65 ->
+  // 6.72. Even at 2 groups on <= 16 K blocks (4096 x 2048 at m = 64: 5.64 -> 5.71, 3072 x 1536 4.96 ->
+  // 4.89) and slower on 56 K blocks (2112 x 7168 at m = 64: 10.21 -> 11.85 with 2 groups, 1536 x 7168 9.02
+  // -> 9.09 with 4), where the K splits make more workgroups.
+  if (pre && m <= 128 && KB >= 16 && KB <= 32) {
+    const int64_t rt = (m + 31) / 32;
+    for (const int kw : {4, 2}) {
+      if (kw == 2 && KB < 24) break;
+      const int64_t wgs = (n + 64 / kw - 1) / (64 / kw);
+      if (wgs * rt > 256) continue;
+      p = Plan8{};
+      p.kind = Kernel8::kStream;
+      p.mt = 2;
+      p.nt = 1;
+      p.nw = 4;
+      p.kw = kw;
+      p.rt = (int)rt;
+      p.grid_x = (int)wgs;
+      finish_splits(p, KB, 1);
+      return true;
+    }
+  }
   if (KB > (m > 128 ? 16 : 64)) return false;
   const int mt = m <= 64 ? 2 : 4;  // 32-row blocks at m = 33..64, 64-row blocks above
   const int64_t rt = (m + mt * 16 - 1) / (mt * 16);

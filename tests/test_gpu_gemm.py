@@ -307,7 +307,9 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
 # 5 at 1536 x 7168, the last holding 8; 7 at 576 x 7168); a second block of one row (m = 65 and 33), a
 # last block of 8 rows (m = 200) and of 18 (m = 50), ragged n (4112: the last group holds 16 columns),
 # fp16 output, row-major weights on the 2-wave plan (3072 x 1536 at m = 64, 100 and 128, with bias; 2048 x
-# 2048 at m = 64 with 2 K splits), and
+# 2048 at m = 64 with 2 K splits), 32-row blocks whose waves split K at 16..32 K blocks (4 groups: 512 x
+# 4096 at m = 64, 1024 x 4096 at m = 128, 2048 x 2048 at m = 50, 1040 x 3072 at m = 40 with a last column
+# group of 16; 2 groups: 1536 x 4096 at m = 96, 2048 x 4096 at m = 128), and
 # row-major weights at 32 K blocks, which keep the 8-row-tile stream plan. Every output compared.
 @pytest.mark.parametrize("m,n,k,variant,bias,fp16,stream", [
     (128, 7168, 2048, "b_shuffled", False, False, True),
@@ -333,6 +335,12 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
     (100, 3072, 1536, "row_major", False, True, True),
     (128, 3072, 1536, "row_major", True, False, True),
     (64, 2048, 2048, "row_major", False, False, True),
+    (64, 512, 4096, "b_shuffled", False, False, True),
+    (128, 1024, 4096, "b_shuffled", False, True, True),
+    (96, 1536, 4096, "b_shuffled", False, False, True),
+    (50, 2048, 2048, "b_shuffled", False, False, True),
+    (128, 2048, 4096, "b_shuffled", False, False, True),
+    (40, 1040, 3072, "b_shuffled", False, True, True),
 ])
 def test_row_block_plans(m, n, k, variant, bias, fp16, stream):
     layout = aklr_amd._lib.B_ROW_MAJOR if variant == "row_major" else aklr_amd._lib.B_PRESHUFFLE_16x16

@@ -50,7 +50,7 @@ def _sample(m, n, rows=64, cols=512, seed=0):
 # split 4 ways (m = 256, n = 2112), the LDS 128x128 plan of a small n, and the stream kernel's row blocks
 # split 2 ways (m = 250, n = 1024: 4 blocks; m = 100, n = 4096: 2).
 FP8_SPLIT = [(16, 4096, 16384), (128, 2112, 7168), (256, 2112, 7168), (300, 1024, 2048), (250, 1024, 2048),
-             (100, 4096, 8192), (96, 576, 7168), (64, 2112, 7168), (50, 4096, 4096),
+             (100, 4096, 8192), (96, 576, 7168), (64, 2112, 7168), (50, 4096, 8192),
              (256, 512, 4096), (1000, 512, 4096)]
 
 
