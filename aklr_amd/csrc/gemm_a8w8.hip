@@ -1289,13 +1289,19 @@ static Plan8 plan8(int64_t m, int64_t n, int64_t k, bool pre, bool fill = true) 
   return plan8_lds_best(m, n, k);
 }
 
-// The LDS kernel's output stores are non-temporal unless the output's row pitch is 8 or 16 KiB.
+// The LDS kernel's output stores are non-temporal unless the output's row pitch is 16 KiB, or 8 KiB on
+// K > 4 blocks.
 // Measured on cold b_shuffled operands (us, cached -> non-temporal stores, both whole lines): 64 KiB
 // pitch (n = 32768, k = 1024) 250 -> 190 at m = 4096 and 107 -> 100 at m = 2048; 48 KiB (24576 x 1536)
 // 195 -> 176-183; 32 KiB at m = 8192 (k = 1024) 229 -> 181; 14 KiB (7168 x 2048) 70.9 -> 68.8; 6 KiB
 // (3072 x 1536, m = 8192) 52.3 -> 49.5. At 16 KiB they lost: 91.7 -> 99.7 (8192 x 8192 x 1024) and
-// 48.0 -> 51.3 (4096 x 8192 x 1024); at 8 KiB 48.8 -> 51.9 (8192 x 4096 x 1024).
-static bool lds_nt_out(int64_t ldo_bytes) { return ldo_bytes != 8192 && ldo_bytes != 16384; }
+// 48.0 -> 51.3 (4096 x 8192 x 1024); at 8 KiB 48.8 -> 51.9 (8192 x 4096 x 1024). On K <= 4 blocks, where
+// the output write is most of the kernel, they won at 8 KiB: 2048 x 4096 x 256 10.5 -> 9.3, x 512 12.7 ->
+// 11.6, 1024 x 4096 x 256 / 512 7.4 / 8.7 -> 7.1 / 8.3, 4096 x 4096 x 256 15.0 -> 14.5 (at 16 KiB mixed:
+// 4096 x 8192 x 512 35.0 -> 37.7, 1024 x 8192 x 512 12.8 -> 11.8).
+static bool lds_nt_out(int64_t ldo_bytes, int64_t k) {
+  return ldo_bytes != 16384 && (ldo_bytes != 8192 || k <= 4 * 128);
+}
 
 static size_t workspace8(const Plan8& p) {
   if (p.splits <= 1) return 0;
@@ -1482,7 +1488,7 @@ int aklr::gemm8_entry(const void* a, int64_t lda, const void* b, int64_t ldb, co
   g.n = (int)n;
   g.k = (int)k;
   g.out_dtype = out_dtype;
-  g.nt_out = lds_nt_out(ldo * 2) ? 1 : 0;
+  g.nt_out = lds_nt_out(ldo * 2, k) ? 1 : 0;
   g.counters = nullptr;
   g.partial = nullptr;
   const bool pre = b_layout == AKLR_B_PRESHUFFLE_16x16;

@@ -353,7 +353,8 @@ def test_row_block_plans(m, n, k, variant, bias, fp16, stream):
 # 4096, 512 x 1024 x 4096 / 1000 x 512 x 4096 / 777 x 1024 x 4096 and 384 x 2048 x 3072), 64x128 unsplit
 # (512 x 4096 x 1024; 300 x 4112 x 2048 with a ragged last row tile of 44 rows and a last column tile of
 # 16) and with 3 and 4 K splits (2112 x 7168 at m = 256, 200 and 192: last column tiles of 64, and at
-# m = 200 a last row tile of 8); both layouts, bias, fp16 and e5m2. Every output compared.
+# m = 200 a last row tile of 8); on 2-4 K blocks at a row pitch of 8 KiB (1024 x 4096 x 512, 2048 x 4096 x
+# 256), whose output stores are non-temporal; both layouts, bias, fp16 and e5m2. Every output compared.
 @pytest.mark.parametrize("m,n,k,variant,bias,fp16,e5", [
     (256, 512, 4096, "b_shuffled", False, False, False),
     (512, 1024, 4096, "row_major", True, True, False),
@@ -365,6 +366,8 @@ def test_row_block_plans(m, n, k, variant, bias, fp16, stream):
     (256, 2112, 7168, "b_shuffled", False, False, False),
     (192, 2112, 7168, "b_shuffled", False, True, False),
     (200, 2112, 7168, "row_major", True, False, False),
+    (1024, 4096, 512, "b_shuffled", False, False, False),
+    (2048, 4096, 256, "row_major", True, True, False),
 ])
 def test_small_output_lds_plans(m, n, k, variant, bias, fp16, e5):
     layout = aklr_amd._lib.B_ROW_MAJOR if variant == "row_major" else aklr_amd._lib.B_PRESHUFFLE_16x16
