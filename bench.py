@@ -261,7 +261,8 @@ REFERENCE_RECORDED = [
 
 
 # Every point the reference records for gemm_a8w8_blockwise_scaled at m >= 64 (below that its times sit on
-# its timer's floor): (n, k, variant, schema directory under aklr/ops/gemm/impls/, [(m, us, file:line)]).
+# its timer's floor), all three layout variants: (n, k, variant, schema directory under
+# aklr/ops/gemm/impls/, [(m, us, file:line)]).
 # bench.py --probe-reference-all runs them all; the default run times REFERENCE_RECORDED above.
 REFERENCE_ALL = [
     (1024, 4096, "b_shuffled", "flydsl/gemm_a8w8_blockwise_scaled_b_shuffled_n1024_k4096", [
@@ -330,7 +331,42 @@ REFERENCE_ALL = [
     (7168, 2048, "row_major", "triton/gemm_a8w8_blockwise_scaled_n7168_k2048", [
         (64, 6.28, "06755ba3ee5eb085.json:105"), (128, 8.18, "1bbf98a368b3fcba.json:105"),
         (256, 11.2, "fee7e092eab87fc5.json:105")]),
+    (1024, 4096, "b_shuffled_row_major_a_scale", "flydsl/gemm_a8w8_blockwise_scaled_b_shuffled_row_major_a_scale_n1024_k4096", [
+        (64, 5.2, "f5b24e49c1568873.json:153"), (128, 6.06, "f5b24e49c1568873.json:161"),
+        (256, 7.7, "f5b24e49c1568873.json:169"), (512, 9.06, "f5b24e49c1568873.json:177"),
+        (1024, 12.1, "f5b24e49c1568873.json:185"), (2048, 15.7, "f5b24e49c1568873.json:193"),
+        (4096, 24.8, "f5b24e49c1568873.json:201")]),
+    (4096, 256, "b_shuffled_row_major_a_scale", "flydsl/gemm_a8w8_blockwise_scaled_b_shuffled_row_major_a_scale_n4096_k256", [
+        (64, 4.12, "5ca82f252cc497e6.json:153"), (128, 4.14, "5ca82f252cc497e6.json:161"),
+        (256, 4.13, "5ca82f252cc497e6.json:169"), (512, 4.3, "5ca82f252cc497e6.json:177"),
+        (1024, 4.38, "5ca82f252cc497e6.json:185"), (2048, 7.47, "5ca82f252cc497e6.json:193"),
+        (4096, 12.4, "5ca82f252cc497e6.json:201")]),
+    (4096, 512, "b_shuffled_row_major_a_scale", "flydsl/gemm_a8w8_blockwise_scaled_b_shuffled_row_major_a_scale_n4096_k512", [
+        (64, 4.67, "d9b93d11ae82adf7.json:153"), (128, 4.73, "d9b93d11ae82adf7.json:161"),
+        (256, 4.54, "d9b93d11ae82adf7.json:169"), (512, 4.65, "d9b93d11ae82adf7.json:177"),
+        (1024, 6.18, "d9b93d11ae82adf7.json:185"), (2048, 9.4, "d9b93d11ae82adf7.json:193"),
+        (4096, 16.0, "d9b93d11ae82adf7.json:201")]),
+    (512, 4096, "b_shuffled_row_major_a_scale", "flydsl/gemm_a8w8_blockwise_scaled_b_shuffled_row_major_a_scale_n512_k4096", [
+        (64, 4.69, "28f1ec94b60ce6b4.json:153"), (128, 5.12, "28f1ec94b60ce6b4.json:161"),
+        (256, 7.19, "28f1ec94b60ce6b4.json:169"), (512, 6.78, "28f1ec94b60ce6b4.json:177"),
+        (1024, 8.26, "28f1ec94b60ce6b4.json:185"), (2048, 11.8, "28f1ec94b60ce6b4.json:193"),
+        (4096, 17.4, "28f1ec94b60ce6b4.json:201")]),
 ]
+
+
+def _ref_operands(variant, q, s, b, m, k):
+    """(a_scale, b, keyword arguments) of one recorded case: b_shuffled takes aiter's preshuffled b and the
+    column-major a_scale; b_shuffled_row_major_a_scale the same b with a K-major a_scale marked
+    ``is_row_major``; row_major the row-major b with a K-major a_scale."""
+    from aklr_amd import layouts
+
+    if variant == "row_major":
+        return s.view(k // 128, m).t().contiguous(), b, {}
+    if variant == "b_shuffled_row_major_a_scale":
+        sa = s.view(k // 128, m).t().contiguous()
+        sa.is_row_major = True
+        return sa, layouts.shuffle_weight(b), {"operand_format": "none:preshuffled"}
+    return s.view(m, k // 128), layouts.shuffle_weight(b), {"operand_format": "none:preshuffled"}
 
 
 def reference_all_cases():
@@ -349,7 +385,7 @@ def reference_recorded_figures(dev, stream, steps=7, cases=None):
     figure: the median kernel duration from the committed rocprofv3 kernel trace of
     ``bench.py --probe-reference`` (the kind of figure the reference's tracer records), when present."""
     import aklr_amd
-    from aklr_amd import layouts, workloads
+    from aklr_amd import workloads
 
     try:
         with open(REFERENCE_TRACE_FILE) as f:
@@ -363,18 +399,13 @@ def reference_recorded_figures(dev, stream, steps=7, cases=None):
             x = workloads.activations(m, k, seed=300 + r, device=dev)
             q, s = aklr_amd.per_group_quant_fp8(x)
             b, bs = workloads.blockwise_fp8_weight(n, k, seed=400 + r, device=dev)
-            if variant == "b_shuffled":
-                copies.append((q, s.view(m, k // 128), layouts.shuffle_weight(b), bs))
-            else:
-                copies.append((q, s.view(k // 128, m).t().contiguous(), b, bs))
+            sa, bb, kw = _ref_operands(variant, q, s, b, m, k)
+            copies.append((q, sa, bb, bs, kw))
             del x
 
-        def run(copies=copies, variant=variant):
-            for q, s, b, bs in copies:
-                if variant == "b_shuffled":
-                    aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s, bs, operand_format="none:preshuffled")
-                else:
-                    aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s, bs)
+        def run(copies=copies):
+            for q, sa, bb, bs, kw in copies:
+                aklr_amd.gemm_a8w8_blockwise_scaled(q, bb, sa, bs, **kw)
         g = _capture(run, stream)
         t = _replay_median_ms(g, steps, 1, stream) / len(copies) * 1e3  # median, as the reference reports
         del g, copies
@@ -712,7 +743,7 @@ def probe_reference(dev, stream, calls=5, cases=None):
     given cases), once per rotating cold operand copy and then ``calls`` more times (rocprofv3
     --kernel-trace gives each launch's duration, the kind of figure the reference's own tracer records)."""
     import aklr_amd
-    from aklr_amd import layouts, workloads
+    from aklr_amd import workloads
 
     plan = []
     for (m, n, k, variant, ref_us, src) in (REFERENCE_RECORDED if cases is None else cases):
@@ -721,18 +752,13 @@ def probe_reference(dev, stream, calls=5, cases=None):
             x = workloads.activations(m, k, seed=300 + r, device=dev)
             q, s = aklr_amd.per_group_quant_fp8(x)
             b, bs = workloads.blockwise_fp8_weight(n, k, seed=400 + r, device=dev)
-            if variant == "b_shuffled":
-                copies.append((q, s.view(m, k // 128), layouts.shuffle_weight(b), bs))
-            else:
-                copies.append((q, s.view(k // 128, m).t().contiguous(), b, bs))
+            sa, bb, kw = _ref_operands(variant, q, s, b, m, k)
+            copies.append((q, sa, bb, bs, kw))
             del x, b
         torch.cuda.synchronize()
         for i in range(len(copies) + calls):
-            q, s, b, bs = copies[i % len(copies)]
-            if variant == "b_shuffled":
-                aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s, bs, operand_format="none:preshuffled")
-            else:
-                aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s, bs)
+            q, sa, bb, bs, kw = copies[i % len(copies)]
+            aklr_amd.gemm_a8w8_blockwise_scaled(q, bb, sa, bs, **kw)
         torch.cuda.synchronize()
         plan.append({"case": f"{m}x{n}x{k} {variant}", "m": m, "n": n, "k": k, "variant": variant,
                      "reference_us": ref_us, "kernels": ["gemm8_"], "launches": len(copies) + calls,
