@@ -376,6 +376,34 @@ def test_small_output_lds_plans(m, n, k, variant, bias, fp16, e5):
                    dtype=torch.float8_e5m2 if e5 else torch.float8_e4m3fn, seed=m + 900, rows=m, cols=n)
 
 
+# The LDS kernel with a K-major a_scale (each stage's scale load strided by the row pitch) against a
+# column-major one (contiguous): the same scale values in the same fold order, so bitwise the same
+# outputs; preshuffled weights (K-major a_scale marked is_row_major) and row-major weights
+# (scale_major_mode K against MN). 64x64, 64x128, 128x128 and 128x192 tiles, 1-4 K splits, a ragged last
+# row tile (1000, 300) and column tile (4112).
+@pytest.mark.parametrize("m,n,k", [(256, 512, 4096), (1000, 512, 4096), (512, 4096, 1024), (1024, 1024, 4096),
+                                   (300, 4112, 2048), (1024, 1536, 4096), (256, 2112, 7168), (1024, 4096, 4096)])
+def test_lds_k_major_a_scale_bitwise(m, n, k):
+    L = aklr_amd._lib.lib()
+    assert L.aklr_gemm_a8w8_blockscale_kernel(m, n, k, aklr_amd._lib.B_PRESHUFFLE_16x16) == 1
+    say(f"gemm_a8w8 K-major a_scale m={m} n={n} k={k}")
+    q, s, b, bs = _fp8_inputs(m, n, k, m + 950, torch.float8_e4m3fn)  # s: [k / 128, m] group-major
+    bb = layouts.shuffle_weight(b)
+    out_cm = aklr_amd.gemm_a8w8_blockwise_scaled(q, bb, s.view(m, k // 128), bs, operand_format="none:preshuffled")
+    sk = s.t().contiguous()
+    sk.is_row_major = True
+    out_km = aklr_amd.gemm_a8w8_blockwise_scaled(q, bb, sk, bs, operand_format="none:preshuffled")
+    assert torch.equal(out_cm.view(torch.int16), out_km.view(torch.int16)), "preshuffled: K-major a_scale differs"
+    out_rk = aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s.t().contiguous(), bs)
+    out_rmn = aklr_amd.gemm_a8w8_blockwise_scaled(q, b, s, bs, scale_major_mode="MN")
+    assert torch.equal(out_rk.view(torch.int16), out_rmn.view(torch.int16)), "row-major: K-major a_scale differs"
+    r, c = _sample(m, n, 64, 512, seed=m)
+    ref = ogemm.gemm_a8w8_blockwise_scaled(u8(q), u8(b), s.cpu().numpy(), bs.cpu().numpy(), scale_major_mode="MN",
+                                           rows=r, cols=c)
+    got = f32(out_km)[np.ix_(r, c)]
+    assert ogemm.within_north_star(got, ref) and ogemm.within_contract_tolerance(got, ref)
+
+
 # The long-K plan (one row tile, >= 96 K blocks, 192-256 workgroups of 32 columns, one K split, each
 # workgroup starting its K walk at its own block): a ragged last workgroup (n = 6160: its second column
 # tile past n) at a K range that 193 workgroups do not divide, 256 workgroups at 100 K blocks, MN scales,
