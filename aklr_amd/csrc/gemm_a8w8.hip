@@ -99,10 +99,20 @@ struct XStage {
 // order, which also spreads neighbouring groups over the 8 XCDs: the logical order measured 3-5% slower
 // there (M = 128 on 7168 x 2048 7.99 -> 8.32, on 3072 x 1536 6.08 -> 6.39; M = 256 on 8192 x 1024 7.18 ->
 // 7.54).
-template <int MT, int NT, int NW, int D, int NS, int FMT, bool PRE, bool QA = false, int KW = 1, bool ROT = false>
+//
+// KS (a K-major a_scale, K contiguous per row): a stage's a_scale load takes 16 rows x 4 consecutive K
+// blocks (16 cache lines) instead of one K block of 64 rows (64 lines, one a row: as many line lookups
+// as the stage's A codes, on the loader's critical path). Groups of 4 K blocks (all rows) then live in
+// a 3-slot LDS ring: the 4 stages of group q each carry a quarter of group q + 1 (the first group is
+// loaded with stage 0), so a group is whole one stage before its first block is consumed, and its slot
+// is refilled 4 stages after its last block was read (NS <= 5 keeps that ordering under the stage
+// barriers). The loads per stage stay kSRows / 64, as for a column-major a_scale.
+template <int MT, int NT, int NW, int D, int NS, int FMT, bool PRE, bool QA = false, int KW = 1, bool ROT = false,
+          bool KS = false>
 __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p) {
   static_assert(!QA || (MT == 1 && FMT == 0 && NW == 4 && KW == 1), "fused quantization: e4m3, one row tile, 4 waves");
   static_assert(!ROT || (KW == 1 && !QA), "rotated K order: one K group, no fused quantization");
+  static_assert(!KS || (!QA && !ROT && NS <= 5), "K-major a_scale ring: no fused quantization or rotated K order");
   static_assert(NS >= 2 && D >= 1 && MT >= 1 && MT <= 8 && 128 % (NT * 16) == 0 && NW % KW == 0, "stream shape");
   constexpr int kSRows = (MT * 16 + 63) / 64 * 64;     // a_scale floats per K block: whole 64-lane loads
   constexpr int kLoadsA = KW * (2 * MT + kSRows / 64);  // loader loads per stage
@@ -117,6 +127,8 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
   __shared__ float sSB[kNBlk][512];
   __shared__ float sQSink[QA ? 64 : 1];  // fused quantization: landing place of the unused scale stores
   __shared__ f32x4 sRed[KW > 1 ? (NW - kWC) * MT * NT * 64 : 1];  // KW > 1: the groups' partial sums
+  // KS: the a_scale ring, [slot][K group][kSRows][4 K blocks] floats (a fragment's 16 rows 4 floats apart)
+  __shared__ __attribute__((aligned(16))) float sS4[KS ? 3 * KW * kSRows * 4 : 1];
   __shared__ unsigned arrive_slot;
 
   uint32_t bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
@@ -204,7 +216,14 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
       const int row = i * 64 + lane;
       s_off[i] = row < p.m ? (uint32_t)((int64_t)row * p.sa_sm * 4) : kOobOffset;
     }
-    const uint32_t lds_a0 = lds_addr(&sA[0][0]), lds_s0 = lds_addr(&sS[0][0]);
+    const uint32_t lds_a0 = lds_addr(&sA[0][0]), lds_s0 = lds_addr(&sS[0][0]), lds_s4 = lds_addr(&sS4[0]);
+    // KS: quarter u (rows 16 u .. + 15) of group q of K group j (step blocks 4 q .. + 3) into its slot
+    auto ks_load = [&](int j, int q, int u) {
+      const int row = u * 16 + (lane >> 2), tk = 4 * q + (lane & 3), kb = kb_begin + j * steps + tk;
+      const bool on = row < p.m && tk < steps && kb < kb_end;
+      lds_dma4(sars, lds_s4 + (((q % 3) * KW + j) * kSRows + u * 16) * 16,
+               on ? (uint32_t)(((int64_t)row * p.sa_sm + (int64_t)kb * p.sa_sk) * 4) : kOobOffset);
+    };
     auto issue = [&](int t, int st) {  // step t: group j's block t, j < KW
 #pragma unroll
       for (int j = 0; j < KW; ++j) {
@@ -218,10 +237,15 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
           for (int h = 0; h < 2; ++h)
             lds_dma16(ars, lds_a0 + st * (KW * MT * 2048) + (j * MT + mt) * 2048 + h * 1024,
                       on && a_off[mt][h] != kOobOffset ? a_off[mt][h] + ak : kOobOffset);
+        if constexpr (KS) {
 #pragma unroll
-        for (int i = 0; i < kSRows / 64; ++i)
-          lds_dma4(sars, lds_s0 + (st * KW + j) * (kSRows * 4) + i * 256,
-                   on && s_off[i] != kOobOffset ? s_off[i] + sk : kOobOffset);
+          for (int i = 0; i < kSRows / 64; ++i) ks_load(j, t / 4 + 1, t % 4 + 4 * i);
+        } else {
+#pragma unroll
+          for (int i = 0; i < kSRows / 64; ++i)
+            lds_dma4(sars, lds_s0 + (st * KW + j) * (kSRows * 4) + i * 256,
+                     on && s_off[i] != kOobOffset ? s_off[i] + sk : kOobOffset);
+        }
       }
     };
     // Stage kb lives in slot (kb - kb_begin) % NS, and all NS slots start filled. A first barrier
@@ -242,6 +266,12 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
         for (int j0 = 0; j0 < len; j0 += 64)
           lds_dma4(sbrs, lds_addr(&sSB[r][j0]), j0 + lane < len ? (uint32_t)((row0 + j0 + lane) * 4) : kOobOffset);
       }
+    }
+    if constexpr (KS) {  // the first a_scale group, whole, with stage 0
+#pragma unroll
+      for (int j = 0; j < KW; ++j)
+#pragma unroll
+        for (int u = 0; u < kSRows / 16; ++u) ks_load(j, 0, u);
     }
 #pragma unroll
     for (int s = 1; s < NS; ++s) issue(s, s);  // only stage loads from here: the counts are exact
@@ -372,14 +402,17 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
     constexpr bool kLineA = !QA;
     const int fa_lo = kLineA ? li * 128 + ((g ^ (li & 7)) << 4) : lane * 16;
     const int fa_hi = kLineA ? li * 128 + (((4 + g) ^ (li & 7)) << 4) : 1024 + lane * 16;
-    auto read_frags = [&](int mt, int slot) {
+    auto read_frags = [&](int mt, int slot, int t) {  // t: the block's step (KS: its a_scale group and place)
       af[mt] = cat(*reinterpret_cast<const u32x4*>(&sA[slot][(kw * MT + mt) * 2048 + fa_lo]),
                    *reinterpret_cast<const u32x4*>(&sA[slot][(kw * MT + mt) * 2048 + fa_hi]));
-      s[mt] = sS[slot][kw * kSRows + mt * 16 + li];
+      if constexpr (KS)
+        s[mt] = sS4[((((t >> 2) % 3) * KW + kw) * kSRows + mt * 16 + li) * 4 + (t & 3)];
+      else
+        s[mt] = sS[slot][kw * kSRows + mt * 16 + li];
     };
     stage_barrier();  // publishes stage kb_begin
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) read_frags(mt, 0);
+    for (int mt = 0; mt < MT; ++mt) read_frags(mt, 0, 0);
     int st = 0;  // slot of stage kb + 1 during block kb
     auto step = [&](int kb, StreamFrag<NT>& f, XStage<MT>& xq) {
       stage_barrier();  // publishes stage kb + 1; every wave is done reading stage kb
@@ -405,7 +438,7 @@ __global__ __launch_bounds__((NW + 1) * 64) void gemm8_stream_kernel(Gemm8Args p
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(part[r], sc, acc[mt][nt][r]);
         }
-        read_frags(mt, st);  // block kb + 1 (past the K range: the zeros of an empty stage)
+        read_frags(mt, st, kb + 1 - kb_begin);  // block kb + 1 (past the K range: the zeros of an empty stage)
       }
       // Interleave: every MFMA after the first is followed by five VALU slots, which take the scale
       // products and the fold FMAs of earlier MFMAs, so the fold runs while the matrix core works.
@@ -1218,7 +1251,19 @@ static Plan8 plan8_stream(int64_t m, int64_t n, int64_t k, bool fill = true) {
 // 15.37 at m = 64) and K > 64 blocks (7168 x 16384 at m = 128: 34.0 -> 40.7) keep the other plans.
 static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p) {
   const int64_t KB = k / 128;
-  if (m <= 32 || m > 256) return false;
+  if (m <= 32 || m > 1024) return false;
+  // m = 257..1024 (preshuffled, 16..32 K blocks): 64-row blocks, the narrowest of 2, 4 and 8 waves that
+  // makes <= 256 workgroups, where the LDS tiles run 16-64 row blocks' worth of 128- or 64-row tiles.
+  // Measured on cold weights, us (the LDS plan -> this): 1024 x 1536 x 4096 21.06 -> 16.32 (8 waves),
+  // 1024 x 2048 x 4096 21.30 -> 16.25, 512 x 4096 x 4096 21.32 -> 16.56, 512 x 2048 x 4096 14.06 -> 11.46
+  // (4 waves), 1024 x 1024 x 4096 13.73 -> 11.52, 512 x 1024 x 4096 11.08 -> 10.16 (2 waves), 1024 x 512 x
+  // 4096 10.92 -> 10.16, 512 x 512 x 4096 9.09 -> 8.73 (2 splits), 768 x 1536 x 4096 16.86 -> 16.09, 384 x
+  // 1536 x 4096 12.76 -> 11.19, 512 x 4096 x 2048 13.02 -> 9.85, 640 x 2048 x 2048 13.98 -> 9.20, 1024 x
+  // 1536 x 2048 12.53 -> 9.81. More than 256 workgroups lost (1024 x 2112 x 4096 24.3 -> 30.5, 1024 x 4096
+  // x 2048 15.9 -> 17.5, 2048 x 1536 x 4096 26.4 -> 32.1), and K = 8192 gained 4% (512 x 1536 x 8192).
+  // Their K splits keep >= 16 K blocks each: 300 x 512 x 2048 on 2 splits 7.01, on one 6.53 (80
+  // workgroups); 512 x 512 x 4096 on 2 splits 8.73, on one 9.96 (128); 1024 x 256 x 4096 9.11 and 9.92.
+  if (m > 256 && (!pre || KB < 16 || KB > 32)) return false;
   // m = 33..128 on 16..32 K blocks (preshuffled weights): 32-row blocks whose 4 waves split K among
   // themselves (4 groups of one wave, 16 columns, while that makes <= 256 workgroups; else 2 groups of
   // two, 32 columns, from 24 K blocks), no K split across workgroups, so no partials. Measured on cold
@@ -1247,17 +1292,18 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
       return true;
     }
   }
-  if (KB > (m > 128 ? 16 : 64)) return false;
+  if (m <= 256 && KB > (m > 128 ? 16 : 64)) return false;
   const int mt = m <= 64 ? 2 : 4;  // 32-row blocks at m = 33..64, 64-row blocks above
   const int64_t rt = (m + mt * 16 - 1) / (mt * 16);
-  static const int kWaves[2][2] = {{2, 4}, {4, 8}};
-  for (const int nw : kWaves[m > 128]) {
-    if (nw == 2 && KB > 16) continue;
+  static const int kWaves[3][3] = {{2, 4, 0}, {4, 8, 0}, {2, 4, 8}};
+  for (const int nw : kWaves[m > 256 ? 2 : (m > 128 ? 1 : 0)]) {
+    if (nw == 0) break;
+    if (nw == 2 && KB > 16 && m <= 256) continue;
     if (!pre && nw != 2) continue;  // row-major weights: the 2-wave plan only
     const int64_t groups = (n + nw * 16 - 1) / (nw * 16);
     if (groups * rt > 256) continue;
     int64_t s = 256 / (groups * rt);
-    if (s > KB / 8) s = KB / 8;
+    if (s > KB / (m > 256 ? 16 : 8)) s = KB / (m > 256 ? 16 : 8);  // m > 256: 16 K blocks a split at least
     if (s < 1) s = 1;
     p = Plan8{};
     p.kind = Kernel8::kStream;
@@ -1320,15 +1366,33 @@ static size_t workspace8_any(int64_t m, int64_t n, int64_t k) {
 // one-wave fill plans and the long-K plan); ring depth 4 at 1-2 row tiles, else 2, and 8 for the long-K
 // plan, 4 and 3 for 7-wave plans of 4 and 8 row tiles at >= 96 K blocks (measured).
 template <int MT, int NT, int FMT, bool PRE, bool QA = false, int KW = 1, int NW = 4, int NS = 4, int DD = 0,
-          bool ROT = false>
+          bool ROT = false, bool KS = false>
 static void launch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   constexpr int D = DD ? DD : (MT <= 2 ? 4 : 2);
-  hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, NW, D, NS, FMT, PRE, QA, KW, ROT>),
+  hipLaunchKernelGGL((gemm8_stream_kernel<MT, NT, NW, D, NS, FMT, PRE, QA, KW, ROT, KS>),
                      dim3((unsigned)d.grid_x, (unsigned)d.splits, (unsigned)d.rt), dim3((NW + 1) * 64), 0, s, a);
 }
 
+// A K-major a_scale (the row-major a_scale variant: e4m3, preshuffled weights) on the 64-row-block plans
+// of >= 24 K blocks a split takes the ring of a_scale quarters (KS). Cold weights, us (column-major
+// a_scale; K-major with per-stage loads -> the ring): 1024 x 1536 x 4096 16.35; 19.05 -> 17.32, 1024 x
+// 1024 x 4096 11.40; 12.63 -> 11.95, 512 x 1024 x 4096 10.18; 10.73 -> 10.56, 1024 x 512 x 4096 10.19;
+// 10.75 -> 10.58. Not taken: 16 K blocks a split (512 x 512 x 4096 on 2 splits 8.95 -> 9.13), 8 (256 x
+// 4096 x 1024 5.77 -> 5.91) and the wave-split 32-row blocks, where the ring measured 2.2-2.4 us slower
+// (64 x 512 x 4096 6.66 -> 8.91, 128 x 1024 x 4096 6.91 -> 8.96, 64 x 4096 x 4096 8.31 -> 9.03) and the
+// per-stage loads cost 2-5% over a column-major a_scale.
 template <int FMT, bool PRE>
 static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
+  if constexpr (FMT == 0 && PRE) {
+    if (a.sa_sk == 1 && a.sa_sm > 1 && !d.rot && d.kb_per_split >= 24) {
+      if (d.kw == 1 && d.mt == 4 && d.dd && (d.nw == 2 || d.nw == 4 || d.nw == 8)) {
+        d.nw == 2   ? launch_stream<4, 1, 0, true, false, 1, 2, 4, 4, false, true>(a, d, s)
+        : d.nw == 4 ? launch_stream<4, 1, 0, true, false, 1, 4, 4, 4, false, true>(a, d, s)
+                    : launch_stream<4, 1, 0, true, false, 1, 8, 4, 4, false, true>(a, d, s);
+        return;
+      }
+    }
+  }
   if (d.kw > 1) {  // one column tile per wave, 1 or 2 row tiles
     if (d.mt == 1) d.kw == 2 ? launch_stream<1, 1, FMT, PRE, false, 2>(a, d, s) : launch_stream<1, 1, FMT, PRE, false, 4>(a, d, s);
     else d.kw == 2 ? launch_stream<2, 1, FMT, PRE, false, 2>(a, d, s) : launch_stream<2, 1, FMT, PRE, false, 4>(a, d, s);

@@ -83,9 +83,13 @@ def test_workspace_sizes_are_host_computable(native_lib):
 def test_gemm8_kernel_query(native_lib):
     # 0: the stream kernel, 1: the LDS kernel, as aklr_gemm_a8w8_blockscale plans (m, n, k) for a layout
     q, row, pre = native_lib.aklr_gemm_a8w8_blockscale_kernel, _lib.B_ROW_MAJOR, _lib.B_PRESHUFFLE_16x16
-    assert q(1, 2112, 7168, row) == 0 and q(128, 24576, 1536, pre) == 0 and q(300, 1024, 2048, pre) == 1
-    # row blocks (preshuffled): m = 65..128 on K <= 64 blocks, m = 129..256 on K <= 16; row-major weights at
-    # m = 65..128 on K <= 16 blocks: 64x64 LDS tiles
+    assert q(1, 2112, 7168, row) == 0 and q(128, 24576, 1536, pre) == 0 and q(300, 1024, 2048, row) == 1
+    # row blocks (preshuffled): m = 65..128 on K <= 64 blocks, m = 129..256 on K <= 16, m = 257..1024 on
+    # 16..32 K blocks while they make <= 256 workgroups; row-major weights at m = 65..128 on K <= 16 blocks:
+    # 64x64 LDS tiles
+    assert q(300, 1024, 2048, pre) == 0 and q(1024, 1536, 4096, pre) == 0 and q(1024, 1536, 4096, row) == 1
+    assert q(1024, 2112, 4096, pre) == 1 and q(1024, 1536, 8192, pre) == 1 and q(1025, 512, 4096, pre) == 1
+    assert q(1024, 1536, 1024, pre) == 1
     assert q(128, 4096, 8192, pre) == 0 and q(128, 4096, 8192, row) == 0
     assert q(128, 7168, 2048, pre) == 0 and q(128, 7168, 2048, row) == 1 and q(64, 7168, 2048, row) == 0
     assert q(256, 7168, 2048, pre) == 0 and q(256, 7168, 2048, row) == 1 and q(256, 2112, 7168, pre) == 1

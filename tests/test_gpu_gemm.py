@@ -309,7 +309,10 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
 # fp16 output, row-major weights on the 2-wave plan (3072 x 1536 at m = 64, 100 and 128, with bias; 2048 x
 # 2048 at m = 64 with 2 K splits), 32-row blocks whose waves split K at 16..32 K blocks (4 groups: 512 x
 # 4096 at m = 64, 1024 x 4096 at m = 128, 2048 x 2048 at m = 50, 1040 x 3072 at m = 40 with a last column
-# group of 16; 2 groups: 1536 x 4096 at m = 96, 2048 x 4096 at m = 128), and
+# group of 16; 2 groups: 1536 x 4096 at m = 96, 2048 x 4096 at m = 128), 64-row blocks at m = 257..1024
+# on 16..32 K blocks (8 waves: 1024 x 1536 x 4096, 640 x 2048 x 2048, 1000 x 1536 x 4096 with a last block
+# of 40 rows; 4 waves: 768 x 1024 x 4096; 2 waves: 300 x 1536 x 4096 with a last block of 44 rows, 512 x
+# 512 x 4096 with 2 K splits), and
 # row-major weights at 32 K blocks, which keep the 8-row-tile stream plan. Every output compared.
 @pytest.mark.parametrize("m,n,k,variant,bias,fp16,stream", [
     (128, 7168, 2048, "b_shuffled", False, False, True),
@@ -341,6 +344,12 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
     (50, 2048, 2048, "b_shuffled", False, False, True),
     (128, 2048, 4096, "b_shuffled", False, False, True),
     (40, 1040, 3072, "b_shuffled", False, True, True),
+    (1024, 1536, 4096, "b_shuffled", False, False, True),
+    (512, 512, 4096, "b_shuffled", False, True, True),
+    (1000, 1536, 4096, "b_shuffled", False, False, True),
+    (640, 2048, 2048, "b_shuffled", False, False, True),
+    (300, 1536, 4096, "b_shuffled", False, True, True),
+    (768, 1024, 4096, "b_shuffled", False, False, True),
 ])
 def test_row_block_plans(m, n, k, variant, bias, fp16, stream):
     layout = aklr_amd._lib.B_ROW_MAJOR if variant == "row_major" else aklr_amd._lib.B_PRESHUFFLE_16x16
@@ -358,9 +367,9 @@ def test_row_block_plans(m, n, k, variant, bias, fp16, stream):
 @pytest.mark.parametrize("m,n,k,variant,bias,fp16,e5", [
     (256, 512, 4096, "b_shuffled", False, False, False),
     (512, 1024, 4096, "row_major", True, True, False),
-    (1000, 512, 4096, "b_shuffled", False, False, False),
+    (1000, 512, 4096, "row_major", False, False, False),
     (777, 1024, 4096, "row_major", False, False, True),
-    (384, 2048, 3072, "b_shuffled", False, True, False),
+    (384, 2048, 3072, "row_major", False, True, False),
     (512, 4096, 1024, "b_shuffled", False, False, False),
     (300, 4112, 2048, "row_major", True, False, False),
     (256, 2112, 7168, "b_shuffled", False, False, False),
@@ -376,16 +385,18 @@ def test_small_output_lds_plans(m, n, k, variant, bias, fp16, e5):
                    dtype=torch.float8_e5m2 if e5 else torch.float8_e4m3fn, seed=m + 900, rows=m, cols=n)
 
 
-# The LDS kernel with a K-major a_scale (each stage's scale load strided by the row pitch) against a
-# column-major one (contiguous): the same scale values in the same fold order, so bitwise the same
-# outputs; preshuffled weights (K-major a_scale marked is_row_major) and row-major weights
-# (scale_major_mode K against MN). 64x64, 64x128, 128x128 and 128x192 tiles, 1-4 K splits, a ragged last
-# row tile (1000, 300) and column tile (4112).
+# A K-major a_scale against a column-major one: the same scale values in the same fold order, so bitwise
+# the same outputs; preshuffled weights (K-major a_scale marked is_row_major) and row-major weights
+# (scale_major_mode K against MN). Preshuffled: the LDS kernel's per-stage loads (64x64, 64x128, 128x128
+# and 128x192 tiles, 1-4 K splits), the stream kernel's ring of 16-row x 4-block a_scale quarters on
+# 64-row blocks of 24-32 K blocks (1000 x 512 and 1024 x 1024 x 4096 on 2 and 4 waves, 1024 x 1536 x 4096
+# on 8, a ragged last row block of 40 rows; 300 x 4112 x 2048, 16 K blocks, takes the per-stage loads),
+# and 32-row blocks whose waves split K (64 x 512 and 128 x 1024 x 4096 in 4 K groups, 100 x 1040 x 3072
+# in 2 over 24 K blocks, ragged rows and columns), per-stage loads.
 @pytest.mark.parametrize("m,n,k", [(256, 512, 4096), (1000, 512, 4096), (512, 4096, 1024), (1024, 1024, 4096),
-                                   (300, 4112, 2048), (1024, 1536, 4096), (256, 2112, 7168), (1024, 4096, 4096)])
-def test_lds_k_major_a_scale_bitwise(m, n, k):
-    L = aklr_amd._lib.lib()
-    assert L.aklr_gemm_a8w8_blockscale_kernel(m, n, k, aklr_amd._lib.B_PRESHUFFLE_16x16) == 1
+                                   (300, 4112, 2048), (1024, 1536, 4096), (256, 2112, 7168), (1024, 4096, 4096),
+                                   (64, 512, 4096), (128, 1024, 4096), (100, 1040, 3072), (600, 768, 3072)])
+def test_k_major_a_scale_bitwise(m, n, k):
     say(f"gemm_a8w8 K-major a_scale m={m} n={n} k={k}")
     q, s, b, bs = _fp8_inputs(m, n, k, m + 950, torch.float8_e4m3fn)  # s: [k / 128, m] group-major
     bb = layouts.shuffle_weight(b)
