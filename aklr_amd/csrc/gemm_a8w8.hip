@@ -610,11 +610,18 @@ constexpr int kLdsGroup = 8;  // tile rows per raster group
 __host__ __device__ constexpr int lds8_stage_a(int tm) { return tm * 128 + (tm + 64) * 4; }
 __host__ __device__ constexpr int lds8_stage_b(int tn) { return tn * 128; }
 
-template <int TM, int TN, int SA, int SB, int FMT, bool PRE>
+// KS (a K-major a_scale, row pitch >= K / 128): the a_scale ring of the stream kernel. An a_scale wave's
+// per-stage load takes 16 of its 64 rows x 4 consecutive K blocks (16 cache lines, not 64) into a 3-slot
+// LDS ring of 4-block groups; stage t carries quarter t % 4 of group t / 4 + 1, the first group goes out
+// before stage 0. A slot is refilled SA stages after the step that read its last block began (SA <= 5),
+// and a group is whole when the first stage of its blocks has landed. Rows past m fall outside the
+// descriptor (the pitch is at least K / 128) and read zeros.
+template <int TM, int TN, int SA, int SB, int FMT, bool PRE, bool KS = false>
 __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   static_assert(TM % 64 == 0 && TM <= 256 && (TN == 64 || TN == 128 || TN == 192 || TN == 224 || TN == 256),
                 "tile shape");
   static_assert(SB >= 2 && (SA == SB || SA == SB + 1), "stage counts");
+  static_assert(!KS || SA <= 5, "a_scale ring: a slot's refill must follow the reads of its last block");
   constexpr int WN = TN == 224 ? 2 : 4, WM = 8 / WN;  // waves along n and m
   constexpr int MT = TM / (16 * WM), NT = TN / (16 * WN);  // 16x16 tiles per wave along m and n
   // TN = 192 (N = 2112 = 11 x 192) and 224 (N = 7168 = 32 x 224): tiles start at multiples of 64 or
@@ -650,6 +657,7 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   __shared__ __attribute__((aligned(16))) float sS[SA * kSStride];
   __shared__ __attribute__((aligned(16))) uint8_t sDummy[1024];  // landing area of the empty loads
   __shared__ unsigned arrive_slot;
+  __shared__ __attribute__((aligned(16))) float sS4[KS ? 3 * TM * 4 : 1];  // KS: [slot][row][4 K blocks]
 
   const int tiles_m = (p.m + TM - 1) / TM;
   const int tiles_n = (p.n + TN - 1) / TN;
@@ -718,7 +726,10 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
       b_off[j] = n0 + r < p.n ? (uint32_t)(r * p.ldb + c * 16) : kOobOffset;
   }
   uint32_t s_off = kOobOffset, s_kstep = 0, lds_s = lds_addr(sDummy), lds_s_step = 0;
-  if (a_scale_wave) {
+  if (KS && a_scale_wave) {
+    s_off = (uint32_t)(((w * 64 + (lane >> 2)) * p.sa_sm + (lane & 3)) * 4);  // quarter 0 of group 0
+    lds_s = lds_addr(&sS4[w * 64 * 4]);
+  } else if (a_scale_wave) {
     if (m0 + w * 64 + lane < p.m) s_off = (uint32_t)((w * 64 + lane) * p.sa_sm * 4);
     s_kstep = (uint32_t)(p.sa_sk * 4);
     lds_s = lds_addr(&sS[w * 64]);
@@ -735,6 +746,13 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   // The lane offsets stay fixed; a stage's K offset rides soffset, so an issue is scalar work only.
   // A stage past the K range loads through a descriptor of no bytes: zeros, no memory traffic, and
   // the same load count.
+  // KS: quarter u (rows 16 u .. + 15 of this wave's 64) of group q into slot q % 3. The whole offset rides
+  // voffset (the descriptor's range check does not cover soffset): blocks past the K range read zeros.
+  auto ks_load = [&](const i32x4& r, int q, int u) {
+    const bool in = 4 * q + (lane & 3) < kb_end - kb_begin;
+    lds_dma4_so(r, lds_s + ((q % 3) * TM + 16 * u) * 16,
+                in ? s_off + (uint32_t)((16 * u * p.sa_sm + kb_begin + 4 * q) * 4) : kOobOffset, 0u);
+  };
   auto issue_a = [&](int kb, int st) {
     const bool on = kb < kb_end;
     i32x4 ra = ars, rs = srs;
@@ -742,7 +760,12 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
     rs[2] = on ? srs[2] : 0;
 #pragma unroll
     for (int j = 0; j < AI; ++j) lds_dma16_so(ra, lds_a + st * kStageA + j * 1024, a_off[j], (uint32_t)kb * 128u);
-    lds_dma4_so(rs, lds_s + st * lds_s_step, s_off, (uint32_t)kb * s_kstep);
+    if (KS && a_scale_wave) {
+      const int t = kb - kb_begin, q = t / 4 + 1, u = t % 4;  // quarter u of group q
+      ks_load(rs, q, u);
+    } else {
+      lds_dma4_so(rs, lds_s + st * lds_s_step, s_off, (uint32_t)kb * s_kstep);
+    }
   };
   auto issue_b = [&](int kb, int st) {
     const bool on = kb < kb_end;
@@ -788,12 +811,13 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
 
   auto kloop = [&](auto split_c) {
     constexpr int SPLIT = decltype(split_c)::value;  // first column tile in block blk0 + 1 (NT: none)
-    auto compute = [&](auto sa_c, auto sb_c) {
+    auto compute = [&](auto sa_c, auto sb_c, int kb) {
       constexpr int STA = decltype(sa_c)::value, STB = decltype(sb_c)::value;
       const uint8_t* A = sA + STA * kStageA;
       const uint8_t* B = sB + STB * kStageB;
       const float* SS = sS + STA * kSStride;
-      const float* SA_ = SS + s_row;
+      const int t4 = kb - kb_begin;  // KS: the block's group t4 / 4 and place t4 % 4
+      const float* SA_ = KS ? sS4 + ((t4 >> 2) % 3) * TM * 4 + s_row * 4 + (t4 & 3) : SS + s_row;
       auto read_a = [&](int mt) {
         return cat(*reinterpret_cast<const u32x4*>(A + a_row + swz_lo + mt * 2048),
                    *reinterpret_cast<const u32x4*>(A + a_row + swz_hi + mt * 2048));
@@ -810,7 +834,7 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
       float sc_lo[MT], sc_hi[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const float sa_row = SA_[mt * 16];
+        const float sa_row = SA_[mt * 16 * (KS ? 4 : 1)];
         sc_lo[mt] = sa_row * sb_lo;
         sc_hi[mt] = SPLIT < NT ? sa_row * sb_hi : 0.f;
       }
@@ -869,7 +893,7 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
       __syncthreads();
       issue_b(kb + SB - 1, (J + SB - 1) % SB);
       issue_a(kb + SA - 1, (J + SA - 1) % SA);
-      compute(IC<J % SA>{}, IC<J % SB>{});
+      compute(IC<J % SA>{}, IC<J % SB>{}, kb);
     };
     constexpr int kRound = SA == SB ? SA : SA * SB;  // SA = SB + 1: coprime
     int kb = kb_begin;
@@ -884,7 +908,11 @@ __global__ __launch_bounds__(512) void gemm8_lds_kernel(Gemm8Args p) {
   };
 
   // Prologue, in the steady state's issue order: with SA = SB + 1, A(0) and then (B(j), A(j + 1)) for
-  // j < SB - 1; with SA = SB, (B(j), A(j)) for j < SB - 1.
+  // j < SB - 1; with SA = SB, (B(j), A(j)) for j < SB - 1. KS: the a_scale waves' first group goes first.
+  if (KS && a_scale_wave) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ks_load(srs, 0, u);
+  }
   if constexpr (SA == SB + 1) issue_a(kb_begin, 0);
 #pragma unroll
   for (int j = 0; j < SB - 1; ++j) {
@@ -1473,15 +1501,34 @@ __host__ __device__ constexpr int lds8_stages(int tm, int tn) {
 __host__ __device__ constexpr bool lds8_fits(int tm, int tn, int sa, int sb) {
   return sa * lds8_stage_a(tm) + sb * lds8_stage_b(tn) + 1024 + 16 <= 160 * 1024;
 }
-template <int TM, int TN, int FMT, bool PRE, int SA = lds8_stages(TM, TN), int SB = lds8_stages(TM, TN)>
+template <int TM, int TN, int FMT, bool PRE, int SA = lds8_stages(TM, TN), int SB = lds8_stages(TM, TN),
+          bool KS = false>
 static void launch_lds_t(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
   static_assert(lds8_fits(TM, TN, SA, SB), "LDS budget");
-  hipLaunchKernelGGL((gemm8_lds_kernel<TM, TN, SA, SB, FMT, PRE>), dim3((unsigned)(t.grid_x * t.splits)), dim3(512),
-                     0, s, a);
+  static_assert(!KS || SA * lds8_stage_a(TM) + SB * lds8_stage_b(TN) + 1024 + 16 + 48 * TM <= 160 * 1024,
+                "LDS budget with the a_scale ring");
+  hipLaunchKernelGGL((gemm8_lds_kernel<TM, TN, SA, SB, FMT, PRE, KS>), dim3((unsigned)(t.grid_x * t.splits)),
+                     dim3(512), 0, s, a);
 }
 
 template <int FMT, bool PRE>
 static void launch_lds(const Gemm8Args& a, const Plan8& t, hipStream_t s) {
+  if constexpr (FMT == 0 && PRE) {
+    // K-major a_scale (pitch >= K / 128) on the 64x64 .. 128x192 tiles: the a_scale ring. Cold operands,
+    // us (column-major a_scale; K-major with per-stage loads -> the ring): 4096 x 1024 x 4096 (128x128, 2
+    // splits) 25.10; 31.47 -> 27.31, 4096 x 512 x 4096 20.83; 23.37 -> 21.62, 2048 x 1024 x 4096 21.11;
+    // 23.26 -> 21.53, 2048 x 512 x 4096 13.77; 15.65 -> 14.48, 2048 x 1536 x 4096 (128x192) 26.70; 29.51 ->
+    // 27.50, 256 x 512 x 4096 (64x64, 4 splits) 8.74; 9.09 -> 9.00, 1500 x 512 x 3584 (64x64) 12.09; 12.46
+    // -> 12.57. On the 128x256 and 192x192 tiles (16 and 18 MFMA tiles a wave) it ran 1.6-2.2x slower
+    // (1100 x 7168 x 2048 26.12 -> 41.69, 2048 x 2112 x 7168 53.04 -> 117.83); the 256-row tiles were not
+    // tried (256x224 and 256x192 have no LDS left for it): those keep the per-stage loads.
+    if (a.sa_sk == 1 && a.sa_sm >= (a.k >> 7)) {
+      if (t.tm == 64 && t.tn == 64) return launch_lds_t<64, 64, 0, true, lds8_stages(64, 64), lds8_stages(64, 64), true>(a, t, s);
+      if (t.tm == 64 && t.tn == 128) return launch_lds_t<64, 128, 0, true, lds8_stages(64, 128), lds8_stages(64, 128), true>(a, t, s);
+      if (t.tm == 128 && t.tn == 128) return launch_lds_t<128, 128, 0, true, lds8_stages(128, 128), lds8_stages(128, 128), true>(a, t, s);
+      if (t.tm == 128 && t.tn == 192) return launch_lds_t<128, 192, 0, true, lds8_stages(128, 192), lds8_stages(128, 192), true>(a, t, s);
+    }
+  }
   if (t.tm == 192) {
     launch_lds_t<192, 192, FMT, PRE>(a, t, s);
   } else if (t.tm == 256) {

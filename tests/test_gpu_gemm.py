@@ -387,15 +387,19 @@ def test_small_output_lds_plans(m, n, k, variant, bias, fp16, e5):
 
 # A K-major a_scale against a column-major one: the same scale values in the same fold order, so bitwise
 # the same outputs; preshuffled weights (K-major a_scale marked is_row_major) and row-major weights
-# (scale_major_mode K against MN). Preshuffled: the LDS kernel's per-stage loads (64x64, 64x128, 128x128
-# and 128x192 tiles, 1-4 K splits), the stream kernel's ring of 16-row x 4-block a_scale quarters on
+# (scale_major_mode K against MN). Preshuffled: the LDS kernel's ring of 16-row x 4-block a_scale
+# quarters (64x64, 64x128, 128x128 and 128x192 tiles, 1-4 K splits, K ranges of 8-32 blocks and of 14
+# at 7168 / 4 splits, whose last group is part empty; 1500 rows: a ragged last row tile) and its
+# per-stage loads (128x256, 192x192 and 256x256 tiles), the stream kernel's ring on
 # 64-row blocks of 24-32 K blocks (1000 x 512 and 1024 x 1024 x 4096 on 2 and 4 waves, 1024 x 1536 x 4096
 # on 8, a ragged last row block of 40 rows; 300 x 4112 x 2048, 16 K blocks, takes the per-stage loads),
 # and 32-row blocks whose waves split K (64 x 512 and 128 x 1024 x 4096 in 4 K groups, 100 x 1040 x 3072
 # in 2 over 24 K blocks, ragged rows and columns), per-stage loads.
 @pytest.mark.parametrize("m,n,k", [(256, 512, 4096), (1000, 512, 4096), (512, 4096, 1024), (1024, 1024, 4096),
                                    (300, 4112, 2048), (1024, 1536, 4096), (256, 2112, 7168), (1024, 4096, 4096),
-                                   (64, 512, 4096), (128, 1024, 4096), (100, 1040, 3072), (600, 768, 3072)])
+                                   (64, 512, 4096), (128, 1024, 4096), (100, 1040, 3072), (600, 768, 3072),
+                                   (1500, 512, 3584), (2048, 1024, 4096), (4096, 512, 4096), (2048, 1536, 4096),
+                                   (2048, 2112, 7168), (1100, 7168, 2048), (1100, 24576, 1536)])
 def test_k_major_a_scale_bitwise(m, n, k):
     say(f"gemm_a8w8 K-major a_scale m={m} n={n} k={k}")
     q, s, b, bs = _fp8_inputs(m, n, k, m + 950, torch.float8_e4m3fn)  # s: [k / 128, m] group-major
