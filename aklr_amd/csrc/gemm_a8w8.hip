@@ -1301,8 +1301,13 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
   // 6.34 / 6.41 / 6.69, 4096 x 4096 9.19 -> 7.90 (2), 2048 x 2048 5.97 -> 5.21; m = 48: 2048 x 4096 7.65 ->
   // 6.72. Even at 2 groups on <= 16 K blocks (4096 x 2048 at m = 64: 5.64 -> 5.71, 3072 x 1536 4.96 ->
   // 4.89) and slower on 56 K blocks (2112 x 7168 at m = 64: 10.21 -> 11.85 with 2 groups, 1536 x 7168 9.02
-  // -> 9.09 with 4), where the K splits make more workgroups.
-  if (pre && m <= 128 && KB >= 16 && KB <= 32) {
+  // -> 9.09 with 4), where the K splits make more workgroups. The same up to m = 1024 while the blocks make
+  // <= 256 workgroups (small N), against the 64x64 LDS tiles with K splits or the 64-row blocks: 256 x 512
+  // x 4096 8.79 -> 6.45 (4 groups), 192 x 512 x 4096 8.46 -> 6.46, 256 x 256 x 4096 8.26 -> 6.36, 256 x 512
+  // x 3072 8.18 -> 5.83, 256 x 1024 x 4096 8.96 -> 7.34 (2 groups), 192 x 1024 x 4096 8.79 -> 7.32, 160 x
+  // 1024 x 4096 8.74 -> 7.23, 200 x 768 x 4096 8.77 -> 7.13, 512 x 512 x 4096 8.78 -> 7.23; more than 256
+  // workgroups lost (256 x 1536 x 4096 11.06 -> 12.82 on 384, 256 x 1024 x 4096 with 4 groups 11.35).
+  if (pre && m <= 1024 && KB >= 16 && KB <= 32) {
     const int64_t rt = (m + 31) / 32;
     for (const int kw : {4, 2}) {
       if (kw == 2 && KB < 24) break;

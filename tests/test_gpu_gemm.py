@@ -311,8 +311,9 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
 # 4096 at m = 64, 1024 x 4096 at m = 128, 2048 x 2048 at m = 50, 1040 x 3072 at m = 40 with a last column
 # group of 16; 2 groups: 1536 x 4096 at m = 96, 2048 x 4096 at m = 128), 64-row blocks at m = 257..1024
 # on 16..32 K blocks (8 waves: 1024 x 1536 x 4096, 640 x 2048 x 2048, 1000 x 1536 x 4096 with a last block
-# of 40 rows; 4 waves: 768 x 1024 x 4096; 2 waves: 300 x 1536 x 4096 with a last block of 44 rows, 512 x
-# 512 x 4096 with 2 K splits), and
+# of 40 rows; 4 waves: 768 x 1024 x 4096; 2 waves: 300 x 1536 x 4096 with a last block of 44 rows), 32-row
+# blocks whose waves split K past m = 128 (4 groups: 256 x 512 x 4096, 192 x 512 x 3072; 2 groups: 512 x 512 x
+# 4096, 200 x 768 x 4096 with a last block of 8 rows, 1024 x 256 x 4096, 300 x 512 x 3072), and
 # row-major weights at 32 K blocks, which keep the 8-row-tile stream plan. Every output compared.
 @pytest.mark.parametrize("m,n,k,variant,bias,fp16,stream", [
     (128, 7168, 2048, "b_shuffled", False, False, True),
@@ -350,6 +351,11 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
     (640, 2048, 2048, "b_shuffled", False, False, True),
     (300, 1536, 4096, "b_shuffled", False, True, True),
     (768, 1024, 4096, "b_shuffled", False, False, True),
+    (256, 512, 4096, "b_shuffled", False, False, True),
+    (192, 512, 3072, "b_shuffled", False, True, True),
+    (200, 768, 4096, "b_shuffled", False, False, True),
+    (1024, 256, 4096, "b_shuffled", False, True, True),
+    (300, 512, 3072, "b_shuffled", False, False, True),
 ])
 def test_row_block_plans(m, n, k, variant, bias, fp16, stream):
     layout = aklr_amd._lib.B_ROW_MAJOR if variant == "row_major" else aklr_amd._lib.B_PRESHUFFLE_16x16
@@ -359,13 +365,13 @@ def test_row_block_plans(m, n, k, variant, bias, fp16, stream):
 
 
 # LDS plans of 64-row tiles where the output is small: 64x64 tiles at 4, 2 and 1 K splits (256 x 512 x
-# 4096, 512 x 1024 x 4096 / 1000 x 512 x 4096 / 777 x 1024 x 4096 and 384 x 2048 x 3072), 64x128 unsplit
+# 5120, 512 x 1024 x 4096 / 1000 x 512 x 4096 / 777 x 1024 x 4096 and 384 x 2048 x 3072), 64x128 unsplit
 # (512 x 4096 x 1024; 300 x 4112 x 2048 with a ragged last row tile of 44 rows and a last column tile of
 # 16) and with 3 and 4 K splits (2112 x 7168 at m = 256, 200 and 192: last column tiles of 64, and at
 # m = 200 a last row tile of 8); on 2-4 K blocks at a row pitch of 8 KiB (1024 x 4096 x 512, 2048 x 4096 x
 # 256), whose output stores are non-temporal; both layouts, bias, fp16 and e5m2. Every output compared.
 @pytest.mark.parametrize("m,n,k,variant,bias,fp16,e5", [
-    (256, 512, 4096, "b_shuffled", False, False, False),
+    (256, 512, 5120, "b_shuffled", False, False, False),
     (512, 1024, 4096, "row_major", True, True, False),
     (1000, 512, 4096, "row_major", False, False, False),
     (777, 1024, 4096, "row_major", False, False, True),
@@ -395,7 +401,7 @@ def test_small_output_lds_plans(m, n, k, variant, bias, fp16, e5):
 # on 8, a ragged last row block of 40 rows; 300 x 4112 x 2048, 16 K blocks, takes the per-stage loads),
 # and 32-row blocks whose waves split K (64 x 512 and 128 x 1024 x 4096 in 4 K groups, 100 x 1040 x 3072
 # in 2 over 24 K blocks, ragged rows and columns), per-stage loads.
-@pytest.mark.parametrize("m,n,k", [(256, 512, 4096), (1000, 512, 4096), (512, 4096, 1024), (1024, 1024, 4096),
+@pytest.mark.parametrize("m,n,k", [(256, 512, 5120), (1000, 512, 4096), (512, 4096, 1024), (1024, 1024, 4096),
                                    (300, 4112, 2048), (1024, 1536, 4096), (256, 2112, 7168), (1024, 4096, 4096),
                                    (64, 512, 4096), (128, 1024, 4096), (100, 1040, 3072), (600, 768, 3072),
                                    (1500, 512, 3584), (2048, 1024, 4096), (4096, 512, 4096), (2048, 1536, 4096),

@@ -52,7 +52,7 @@ def _twice(call, need, what):
 @pytest.mark.parametrize("m,n,k", [(16, 4096, 16384), (128, 2112, 7168), (256, 2112, 7168), (250, 1024, 2048),
                                    (100, 4096, 8192), (96, 576, 7168), (128, 1536, 7168),
                                    (64, 2112, 7168), (50, 4096, 8192),
-                                   (256, 512, 4096), (1000, 512, 8192), (300, 1024, 7168), (512, 512, 4096)])
+                                   (256, 512, 5120), (1000, 512, 8192), (300, 1024, 7168)])
 def test_fp8_split_words_reset(m, n, k):
     L = _lib.lib()
     need = L.aklr_gemm_a8w8_blockscale_workspace_bytes(m, n, k)
