@@ -1325,6 +1325,27 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
       return true;
     }
   }
+  // m = 129..1024 on 24..32 K blocks (preshuffled) where the 32-row blocks above make too many workgroups:
+  // 64-row blocks whose 4 waves form 2 K groups of 2 (32 columns), while those make <= 256 workgroups.
+  // Cold weights, us (the plan before -> this): 256 x 2048 x 4096 11.15 -> 9.98 (LDS 64x64 before), 256 x
+  // 1536 x 4096 10.93 -> 9.84, 1024 x 512 x 4096 10.10 -> 9.80 (64-row blocks of 2 waves before), 512 x
+  // 1024 x 4096 10.14 -> 9.86, 768 x 512 x 4096 9.99 -> 9.80, 384 x 1024 x 4096 10.05 -> 9.77; where the
+  // 32-row blocks fit they are faster (512 x 512 x 4096 7.23 against 9.65).
+  if (pre && m > 128 && m <= 1024 && KB >= 24 && KB <= 32) {
+    const int64_t rt = (m + 63) / 64, wgs = (n + 31) / 32;
+    if (wgs * rt <= 256) {
+      p = Plan8{};
+      p.kind = Kernel8::kStream;
+      p.mt = 4;
+      p.nt = 1;
+      p.nw = 4;
+      p.kw = 2;
+      p.rt = (int)rt;
+      p.grid_x = (int)wgs;
+      finish_splits(p, KB, 1);
+      return true;
+    }
+  }
   if (m <= 256 && KB > (m > 128 ? 16 : 64)) return false;
   const int mt = m <= 64 ? 2 : 4;  // 32-row blocks at m = 33..64, 64-row blocks above
   const int64_t rt = (m + mt * 16 - 1) / (mt * 16);
@@ -1418,16 +1439,16 @@ template <int FMT, bool PRE>
 static void dispatch_stream(const Gemm8Args& a, const Plan8& d, hipStream_t s) {
   if constexpr (FMT == 0 && PRE) {
     if (a.sa_sk == 1 && a.sa_sm > 1 && !d.rot && d.kb_per_split >= 24) {
-      if (d.kw == 1 && d.mt == 4 && d.dd && (d.nw == 2 || d.nw == 4 || d.nw == 8)) {
-        d.nw == 2   ? launch_stream<4, 1, 0, true, false, 1, 2, 4, 4, false, true>(a, d, s)
-        : d.nw == 4 ? launch_stream<4, 1, 0, true, false, 1, 4, 4, 4, false, true>(a, d, s)
-                    : launch_stream<4, 1, 0, true, false, 1, 8, 4, 4, false, true>(a, d, s);
+      if (d.kw == 1 && d.mt == 4 && d.dd && (d.nw == 4 || d.nw == 8)) {  // (2 waves: the K-group plan first)
+        d.nw == 4 ? launch_stream<4, 1, 0, true, false, 1, 4, 4, 4, false, true>(a, d, s)
+                  : launch_stream<4, 1, 0, true, false, 1, 8, 4, 4, false, true>(a, d, s);
         return;
       }
     }
   }
-  if (d.kw > 1) {  // one column tile per wave, 1 or 2 row tiles
+  if (d.kw > 1) {  // one column tile per wave, 1, 2 or 4 row tiles (4: 2 K groups only)
     if (d.mt == 1) d.kw == 2 ? launch_stream<1, 1, FMT, PRE, false, 2>(a, d, s) : launch_stream<1, 1, FMT, PRE, false, 4>(a, d, s);
+    else if (d.mt == 4) launch_stream<4, 1, FMT, PRE, false, 2>(a, d, s);
     else d.kw == 2 ? launch_stream<2, 1, FMT, PRE, false, 2>(a, d, s) : launch_stream<2, 1, FMT, PRE, false, 4>(a, d, s);
   } else if (d.rot) {
     launch_stream<1, 1, FMT, PRE, false, 1, 2, 8, 8, true>(a, d, s);

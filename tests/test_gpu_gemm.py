@@ -311,7 +311,9 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
 # 4096 at m = 64, 1024 x 4096 at m = 128, 2048 x 2048 at m = 50, 1040 x 3072 at m = 40 with a last column
 # group of 16; 2 groups: 1536 x 4096 at m = 96, 2048 x 4096 at m = 128), 64-row blocks at m = 257..1024
 # on 16..32 K blocks (8 waves: 1024 x 1536 x 4096, 640 x 2048 x 2048, 1000 x 1536 x 4096 with a last block
-# of 40 rows; 4 waves: 768 x 1024 x 4096; 2 waves: 300 x 1536 x 4096 with a last block of 44 rows), 32-row
+# of 40 rows; 4 waves: 768 x 1024 x 4096), 64-row blocks of 2 K groups of 2 waves at m = 129..1024 (256 x
+# 2048 and 256 x 1536 x 4096, 200 x 1536 x 3072 and 300 x 1536 x 4096 with last blocks of 8 and 44 rows,
+# 1024 x 512 and 700 x 512 x 4096), 32-row
 # blocks whose waves split K past m = 128 (4 groups: 256 x 512 x 4096, 192 x 512 x 3072; 2 groups: 512 x 512 x
 # 4096, 200 x 768 x 4096 with a last block of 8 rows, 1024 x 256 x 4096, 300 x 512 x 3072), and
 # row-major weights at 32 K blocks, which keep the 8-row-tile stream plan. Every output compared.
@@ -356,6 +358,11 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
     (200, 768, 4096, "b_shuffled", False, False, True),
     (1024, 256, 4096, "b_shuffled", False, True, True),
     (300, 512, 3072, "b_shuffled", False, False, True),
+    (256, 2048, 4096, "b_shuffled", False, True, True),
+    (256, 1536, 4096, "b_shuffled", False, False, True),
+    (200, 1536, 3072, "b_shuffled", False, False, True),
+    (1024, 512, 4096, "b_shuffled", False, True, True),
+    (700, 512, 4096, "b_shuffled", False, False, True),
 ])
 def test_row_block_plans(m, n, k, variant, bias, fp16, stream):
     layout = aklr_amd._lib.B_ROW_MAJOR if variant == "row_major" else aklr_amd._lib.B_PRESHUFFLE_16x16
@@ -397,13 +404,15 @@ def test_small_output_lds_plans(m, n, k, variant, bias, fp16, e5):
 # quarters (64x64, 64x128, 128x128 and 128x192 tiles, 1-4 K splits, K ranges of 8-32 blocks and of 14
 # at 7168 / 4 splits, whose last group is part empty; 1500 rows: a ragged last row tile) and its
 # per-stage loads (128x256, 192x192 and 256x256 tiles), the stream kernel's ring on
-# 64-row blocks of 24-32 K blocks (1000 x 512 and 1024 x 1024 x 4096 on 2 and 4 waves, 1024 x 1536 x 4096
-# on 8, a ragged last row block of 40 rows; 300 x 4112 x 2048, 16 K blocks, takes the per-stage loads),
-# and 32-row blocks whose waves split K (64 x 512 and 128 x 1024 x 4096 in 4 K groups, 100 x 1040 x 3072
-# in 2 over 24 K blocks, ragged rows and columns), per-stage loads.
+# 64-row blocks of 24-32 K blocks (1024 x 1024 x 4096 on 4 waves, 1024 x 1536 x 4096 and 1000 x 1536 x
+# 4096 on 8, a ragged last row block of 40 rows; 300 x 4112 x 2048, 16 K blocks, takes the per-stage
+# loads), and per-stage loads on the blocks whose waves split K (32-row: 64 x 512 and 128 x 1024 x 4096 in
+# 4 K groups, 100 x 1040 x 3072 in 2 over 24 K blocks, ragged rows and columns; 64-row: 1000 x 512 x 4096
+# and 600 x 768 x 3072, ragged last blocks of 40 and 24 rows).
 @pytest.mark.parametrize("m,n,k", [(256, 512, 5120), (1000, 512, 4096), (512, 4096, 1024), (1024, 1024, 4096),
                                    (300, 4112, 2048), (1024, 1536, 4096), (256, 2112, 7168), (1024, 4096, 4096),
                                    (64, 512, 4096), (128, 1024, 4096), (100, 1040, 3072), (600, 768, 3072),
+                                   (1000, 1536, 4096),
                                    (1500, 512, 3584), (2048, 1024, 4096), (4096, 512, 4096), (2048, 1536, 4096),
                                    (2048, 2112, 7168), (1100, 7168, 2048), (1100, 24576, 1536)])
 def test_k_major_a_scale_bitwise(m, n, k):
