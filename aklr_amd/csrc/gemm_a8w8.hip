@@ -1307,10 +1307,14 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
   // x 3072 8.18 -> 5.83, 256 x 1024 x 4096 8.96 -> 7.34 (2 groups), 192 x 1024 x 4096 8.79 -> 7.32, 160 x
   // 1024 x 4096 8.74 -> 7.23, 200 x 768 x 4096 8.77 -> 7.13, 512 x 512 x 4096 8.78 -> 7.23; more than 256
   // workgroups lost (256 x 1536 x 4096 11.06 -> 12.82 on 384, 256 x 1024 x 4096 with 4 groups 11.35).
+  // Past m = 128 the 2 groups also take 16..23 K blocks (against the 64-row blocks of 2 waves, us: 512 x
+  // 512 x 2048 6.64 -> 5.32, 1024 x 256 x 2048 6.61 -> 5.25, 300 x 768 x 2048 6.65 -> 5.29, 384 x 512 x 2048
+  // 6.60 -> 5.22, 700 x 256 x 2048 6.53 -> 5.20, 512 x 512 x 2560 7.60 -> 5.82; against the 64-row K-group
+  // blocks: 200 x 1024 x 2048 6.89 -> 5.26, 160 x 1536 x 2048 6.95 -> 5.41).
   if (pre && m <= 1024 && KB >= 16 && KB <= 32) {
     const int64_t rt = (m + 31) / 32;
     for (const int kw : {4, 2}) {
-      if (kw == 2 && KB < 24) break;
+      if (kw == 2 && KB < 24 && m <= 128) break;
       const int64_t wgs = (n + 64 / kw - 1) / (64 / kw);
       if (wgs * rt > 256) continue;
       p = Plan8{};
@@ -1325,13 +1329,16 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
       return true;
     }
   }
-  // m = 129..1024 on 24..32 K blocks (preshuffled) where the 32-row blocks above make too many workgroups:
-  // 64-row blocks whose 4 waves form 2 K groups of 2 (32 columns), while those make <= 256 workgroups.
-  // Cold weights, us (the plan before -> this): 256 x 2048 x 4096 11.15 -> 9.98 (LDS 64x64 before), 256 x
-  // 1536 x 4096 10.93 -> 9.84, 1024 x 512 x 4096 10.10 -> 9.80 (64-row blocks of 2 waves before), 512 x
-  // 1024 x 4096 10.14 -> 9.86, 768 x 512 x 4096 9.99 -> 9.80, 384 x 1024 x 4096 10.05 -> 9.77; where the
-  // 32-row blocks fit they are faster (512 x 512 x 4096 7.23 against 9.65).
-  if (pre && m > 128 && m <= 1024 && KB >= 24 && KB <= 32) {
+  // m = 129..1024 on 24..32 K blocks, and m = 129..256 on 16..23 (preshuffled), where the 32-row blocks
+  // above make too many workgroups: 64-row blocks whose 4 waves form 2 K groups of 2 (32 columns), while
+  // those make <= 256 workgroups. Cold weights, us (the plan before -> this): 256 x 2048 x 4096 11.15 ->
+  // 9.98 (LDS 64x64 before), 256 x 1536 x 4096 10.93 -> 9.84, 1024 x 512 x 4096 10.10 -> 9.80 (64-row
+  // blocks of 2 waves before), 512 x 1024 x 4096 10.14 -> 9.86, 768 x 512 x 4096 9.99 -> 9.80, 384 x 1024 x
+  // 4096 10.05 -> 9.77; 256 x 1536 x 2048 8.42 -> 7.03 (64-row blocks, 2 K splits), 256 x 2048 x 2048 8.59
+  // -> 7.11. On 16 K blocks past m = 256 the unsplit 64-row blocks of 2
+  // waves are faster (512 x 1024 x 2048 6.84 against 7.14, 1024 x 512 x 2048 6.77 against 7.12), and where
+  // the 32-row blocks fit they are (512 x 512 x 4096 7.23 against 9.65).
+  if (pre && m > 128 && m <= 1024 && KB >= (m > 256 ? 24 : 16) && KB <= 32) {
     const int64_t rt = (m + 63) / 64, wgs = (n + 31) / 32;
     if (wgs * rt <= 256) {
       p = Plan8{};

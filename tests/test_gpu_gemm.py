@@ -303,7 +303,7 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
 # blocks; m = 129..256 on K <= 16 blocks), 32-row blocks at m = 33..64 on K <= 64 blocks. 64-column
 # workgroups of 4 waves (32 columns and 2 waves at 3072 x 1536 and m <= 128; 128 columns and 8 waves at
 # 7168 x 2048 and 8192 x 1024 past m = 128), K split into as many parts as keep <= 256 workgroups at >= 8
-# K blocks each (2 at m = 250: 16 workgroups a row block; 3 at 2112 x 7168, the last holding 18 K blocks;
+# K blocks each (3 at 2112 x 7168, the last holding 18 K blocks;
 # 5 at 1536 x 7168, the last holding 8; 7 at 576 x 7168); a second block of one row (m = 65 and 33), a
 # last block of 8 rows (m = 200) and of 18 (m = 50), ragged n (4112: the last group holds 16 columns),
 # fp16 output, row-major weights on the 2-wave plan (3072 x 1536 at m = 64, 100 and 128, with bias; 2048 x
@@ -313,9 +313,11 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
 # on 16..32 K blocks (8 waves: 1024 x 1536 x 4096, 640 x 2048 x 2048, 1000 x 1536 x 4096 with a last block
 # of 40 rows; 4 waves: 768 x 1024 x 4096), 64-row blocks of 2 K groups of 2 waves at m = 129..1024 (256 x
 # 2048 and 256 x 1536 x 4096, 200 x 1536 x 3072 and 300 x 1536 x 4096 with last blocks of 8 and 44 rows,
-# 1024 x 512 and 700 x 512 x 4096), 32-row
+# 1024 x 512 and 700 x 512 x 4096; 256 x 1536 x 2048 on 16 K blocks), 32-row
 # blocks whose waves split K past m = 128 (4 groups: 256 x 512 x 4096, 192 x 512 x 3072; 2 groups: 512 x 512 x
-# 4096, 200 x 768 x 4096 with a last block of 8 rows, 1024 x 256 x 4096, 300 x 512 x 3072), and
+# 4096, 200 x 768 x 4096 with a last block of 8 rows, 1024 x 256 x 4096, 300 x 512 x 3072; on 16-20 K
+# blocks: 250 x 1024 and 512 x 512 x 2048, 300 x 768 x 2048 and 700 x 256 x 2560 with last blocks of 12
+# and 28 rows), and
 # row-major weights at 32 K blocks, which keep the 8-row-tile stream plan. Every output compared.
 @pytest.mark.parametrize("m,n,k,variant,bias,fp16,stream", [
     (128, 7168, 2048, "b_shuffled", False, False, True),
@@ -330,7 +332,11 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
     (192, 7168, 2048, "b_shuffled", False, True, True),
     (200, 3072, 1536, "b_shuffled", False, False, True),
     (256, 8192, 1024, "b_shuffled", False, True, True),
-    (250, 1024, 2048, "b_shuffled", False, False, True),
+    (250, 1024, 2048, "b_shuffled", False, False, True),  # 32-row blocks of 2 K groups, 16 K blocks
+    (512, 512, 2048, "b_shuffled", False, True, True),
+    (300, 768, 2048, "b_shuffled", False, False, True),
+    (700, 256, 2560, "b_shuffled", False, False, True),
+    (256, 1536, 2048, "b_shuffled", False, False, True),
     (64, 3072, 1536, "b_shuffled", False, False, True),
     (33, 7168, 2048, "b_shuffled", False, True, True),
     (64, 2112, 7168, "b_shuffled", False, False, True),

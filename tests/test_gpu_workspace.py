@@ -49,8 +49,8 @@ def _sample(m, n, rows=64, cols=512, seed=0):
 # FP8 plans that split K: stream kernel (m = 16 and 128 at 4 splits), LDS kernel with 128-row tiles
 # split 4 ways (m = 256, n = 2112), the LDS 64-row tiles of a small output (64x64: m = 256, n = 512 at 40
 # K blocks and m = 300, n = 1024 at 56; 64x128: m = 1000, n = 512 at 64 K blocks), and the stream
-# kernel's row blocks split 2 ways (m = 250, n = 1024: 4 blocks; m = 100, n = 4096: 2).
-FP8_SPLIT = [(16, 4096, 16384), (128, 2112, 7168), (256, 2112, 7168), (300, 1024, 7168), (250, 1024, 2048),
+# kernel's row blocks split 2 ways (m = 100, n = 4096: 2 blocks).
+FP8_SPLIT = [(16, 4096, 16384), (128, 2112, 7168), (256, 2112, 7168), (300, 1024, 7168),
              (100, 4096, 8192), (96, 576, 7168), (64, 2112, 7168), (50, 4096, 8192),
              (256, 512, 5120), (1000, 512, 8192)]
 
