@@ -1291,7 +1291,7 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
   // x 2048 15.9 -> 17.5, 2048 x 1536 x 4096 26.4 -> 32.1), and K = 8192 gained 4% (512 x 1536 x 8192).
   // Their K splits keep >= 16 K blocks each: 300 x 512 x 2048 on 2 splits 7.01, on one 6.53 (80
   // workgroups); 512 x 512 x 4096 on 2 splits 8.73, on one 9.96 (128); 1024 x 256 x 4096 9.11 and 9.92.
-  if (m > 256 && (!pre || KB < 16 || KB > 32)) return false;
+  if (m > 256 && (!pre || KB < 8 || KB > 32)) return false;
   // m = 33..128 on 16..32 K blocks (preshuffled weights): 32-row blocks whose 4 waves split K among
   // themselves (4 groups of one wave, 16 columns, while that makes <= 256 workgroups; else 2 groups of
   // two, 32 columns, from 24 K blocks), no K split across workgroups, so no partials. Measured on cold
@@ -1310,10 +1310,14 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
   // Past m = 128 the 2 groups also take 16..23 K blocks (against the 64-row blocks of 2 waves, us: 512 x
   // 512 x 2048 6.64 -> 5.32, 1024 x 256 x 2048 6.61 -> 5.25, 300 x 768 x 2048 6.65 -> 5.29, 384 x 512 x 2048
   // 6.60 -> 5.22, 700 x 256 x 2048 6.53 -> 5.20, 512 x 512 x 2560 7.60 -> 5.82; against the 64-row K-group
-  // blocks: 200 x 1024 x 2048 6.89 -> 5.26, 160 x 1536 x 2048 6.95 -> 5.41).
-  if (pre && m <= 1024 && KB >= 16 && KB <= 32) {
+  // blocks: 200 x 1024 x 2048 6.89 -> 5.26, 160 x 1536 x 2048 6.95 -> 5.41), and 8..15 K blocks with 2
+  // groups only (against the LDS tiles or 64-row blocks, us: 512 x 512 x 1024 6.34 -> 4.31, 1024 x 256 x
+  // 1024 6.13 -> 4.31, 256 x 1024 x 1024 5.32 -> 4.28, 256 x 512 x 1024 5.24 -> 4.21 where 4 groups of 2
+  // blocks gave 4.46, 300 x 768 x 1536 7.59 -> 4.63).
+  if (pre && m <= 1024 && KB <= 32 && KB >= (m > 128 ? 8 : 16)) {
     const int64_t rt = (m + 31) / 32;
     for (const int kw : {4, 2}) {
+      if (kw == 4 && KB < 16) continue;
       if (kw == 2 && KB < 24 && m <= 128) break;
       const int64_t wgs = (n + 64 / kw - 1) / (64 / kw);
       if (wgs * rt > 256) continue;
@@ -1338,7 +1342,9 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
   // -> 7.11. On 16 K blocks past m = 256 the unsplit 64-row blocks of 2
   // waves are faster (512 x 1024 x 2048 6.84 against 7.14, 1024 x 512 x 2048 6.77 against 7.12), and where
   // the 32-row blocks fit they are (512 x 512 x 4096 7.23 against 9.65).
-  if (pre && m > 128 && m <= 1024 && KB >= (m > 256 ? 24 : 16) && KB <= 32) {
+  // On 12..15 K blocks too, at any m here (512 x 1024 x 1536 7.77 -> 6.44 and 1024 x 512 x 1536 7.53 ->
+  // 6.48 against the LDS tiles, 256 x 2048 x 1536 6.52 -> 6.44 against the 64-row blocks).
+  if (pre && m > 128 && m <= 1024 && KB >= 12 && KB <= 32 && !(m > 256 && KB >= 16 && KB < 24)) {
     const int64_t rt = (m + 63) / 64, wgs = (n + 31) / 32;
     if (wgs * rt <= 256) {
       p = Plan8{};
@@ -1353,6 +1359,7 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
       return true;
     }
   }
+  if (m > 256 && KB < 16) return false;  // the 64-row blocks below: 16..32 K blocks past m = 256
   if (m <= 256 && KB > (m > 128 ? 16 : 64)) return false;
   const int mt = m <= 64 ? 2 : 4;  // 32-row blocks at m = 33..64, 64-row blocks above
   const int64_t rt = (m + mt * 16 - 1) / (mt * 16);
