@@ -1313,12 +1313,14 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
   // blocks: 200 x 1024 x 2048 6.89 -> 5.26, 160 x 1536 x 2048 6.95 -> 5.41), and 8..15 K blocks with 2
   // groups only (against the LDS tiles or 64-row blocks, us: 512 x 512 x 1024 6.34 -> 4.31, 1024 x 256 x
   // 1024 6.13 -> 4.31, 256 x 1024 x 1024 5.32 -> 4.28, 256 x 512 x 1024 5.24 -> 4.21 where 4 groups of 2
-  // blocks gave 4.46, 300 x 768 x 1536 7.59 -> 4.63).
-  if (pre && m <= 1024 && KB <= 32 && KB >= (m > 128 ? 8 : 16)) {
+  // blocks gave 4.46, 300 x 768 x 1536 7.59 -> 4.63); the same 2 groups at m = 65..128 on 8..15 K
+  // blocks (against the 4- and 8-row-tile plans: 128 x 512 x 1024 4.91 -> 4.16, 128 x 1024 x 1536 5.91 ->
+  // 4.56, 96 x 768 x 1536 5.84 -> 4.56; at m = 64 those stay faster, 64 x 512 x 1024 3.86 against 4.12).
+  if (pre && m <= 1024 && KB <= 32 && KB >= (m > 64 ? 8 : 16)) {
     const int64_t rt = (m + 31) / 32;
     for (const int kw : {4, 2}) {
       if (kw == 4 && KB < 16) continue;
-      if (kw == 2 && KB < 24 && m <= 128) break;
+      if (kw == 2 && m <= 128 && KB >= 16 && KB < 24) break;
       const int64_t wgs = (n + 64 / kw - 1) / (64 / kw);
       if (wgs * rt > 256) continue;
       p = Plan8{};
