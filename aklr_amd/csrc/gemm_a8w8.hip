@@ -1345,8 +1345,11 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
   // waves are faster (512 x 1024 x 2048 6.84 against 7.14, 1024 x 512 x 2048 6.77 against 7.12), and where
   // the 32-row blocks fit they are (512 x 512 x 4096 7.23 against 9.65).
   // On 12..15 K blocks too, at any m here (512 x 1024 x 1536 7.77 -> 6.44 and 1024 x 512 x 1536 7.53 ->
-  // 6.48 against the LDS tiles, 256 x 2048 x 1536 6.52 -> 6.44 against the 64-row blocks).
-  if (pre && m > 128 && m <= 1024 && KB >= 12 && KB <= 32 && !(m > 256 && KB >= 16 && KB < 24)) {
+  // 6.48 against the LDS tiles, 256 x 2048 x 1536 6.52 -> 6.44 against the 64-row blocks), and on 8..11
+  // past m = 256 (against the LDS tiles: 512 x 1024 x 1024 6.44 -> 5.79, 1024 x 512 x 1024 6.23 -> 5.77,
+  // 768 x 640 x 1024 6.32 -> 6.02; at m = 256 the 64-row blocks of 4 waves stay faster, 256 x 1024 x 1024
+  // 5.32 against 5.58, and past 256 workgroups it lost: 600 x 1024 x 1280 6.94 -> 9.70 on 320).
+  if (pre && m > 128 && m <= 1024 && KB >= (m > 256 ? 8 : 12) && KB <= 32 && !(m > 256 && KB >= 16 && KB < 24)) {
     const int64_t rt = (m + 63) / 64, wgs = (n + 31) / 32;
     if (wgs * rt <= 256) {
       p = Plan8{};

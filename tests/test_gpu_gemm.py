@@ -319,7 +319,8 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
 # blocks: 250 x 1024 and 512 x 512 x 2048, 300 x 768 x 2048 and 700 x 256 x 2560 with last blocks of 12
 # and 28 rows; on 8-12 K blocks, 2 groups: 512 x 512, 256 x 512 and 128 x 512 x 1024, 300 x 768 and 100 x
 # 1024 x 1536; 64-row blocks
-# of 2 K groups on 12: 1024 x 512 and 256 x 2048 x 1536), and
+# of 2 K groups on 12: 1024 x 512 and 256 x 2048 x 1536, on 8: 512 x 1024 and 700 x 640 x 1024, a last
+# block of 60 rows), and
 # row-major weights at 32 K blocks, which keep the 8-row-tile stream plan. Every output compared.
 @pytest.mark.parametrize("m,n,k,variant,bias,fp16,stream", [
     (128, 7168, 2048, "b_shuffled", False, False, True),
@@ -346,6 +347,8 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
     (256, 2048, 1536, "b_shuffled", False, True, True),
     (128, 512, 1024, "b_shuffled", False, False, True),
     (100, 1024, 1536, "b_shuffled", False, True, True),
+    (512, 1024, 1024, "b_shuffled", False, False, True),
+    (700, 640, 1024, "b_shuffled", False, True, True),
     (64, 3072, 1536, "b_shuffled", False, False, True),
     (33, 7168, 2048, "b_shuffled", False, True, True),
     (64, 2112, 7168, "b_shuffled", False, False, True),
