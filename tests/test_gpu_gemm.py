@@ -320,7 +320,9 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
 # and 28 rows; on 8-12 K blocks, 2 groups: 512 x 512, 256 x 512 and 128 x 512 x 1024, 300 x 768 and 100 x
 # 1024 x 1536; 64-row blocks
 # of 2 K groups on 12: 1024 x 512 and 256 x 2048 x 1536, on 8: 512 x 1024 and 700 x 640 x 1024, a last
-# block of 60 rows), and
+# block of 60 rows; edges: 129 x 48 x 4096 (a last block of one row, 3 groups of 16 columns), 1024 x 16 x
+# 1024 (one group), 1000 x 80 x 1536 (a last group of 16 columns, a last block of 8 rows); 257 x 2064 x
+# 3072 on 64-row blocks of 4 waves, a last block of one row and a last group of 16 columns), and
 # row-major weights at 32 K blocks, which keep the 8-row-tile stream plan. Every output compared.
 @pytest.mark.parametrize("m,n,k,variant,bias,fp16,stream", [
     (128, 7168, 2048, "b_shuffled", False, False, True),
@@ -349,6 +351,10 @@ def test_64_row_tiles(m, n, k, bias, fp16, e5):
     (100, 1024, 1536, "b_shuffled", False, True, True),
     (512, 1024, 1024, "b_shuffled", False, False, True),
     (700, 640, 1024, "b_shuffled", False, True, True),
+    (129, 48, 4096, "b_shuffled", False, False, True),
+    (1024, 16, 1024, "b_shuffled", False, True, True),
+    (1000, 80, 1536, "b_shuffled", False, False, True),
+    (257, 2064, 3072, "b_shuffled", False, False, True),
     (64, 3072, 1536, "b_shuffled", False, False, True),
     (33, 7168, 2048, "b_shuffled", False, True, True),
     (64, 2112, 7168, "b_shuffled", False, False, True),
