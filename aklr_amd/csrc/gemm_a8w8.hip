@@ -1291,6 +1291,8 @@ static bool plan8_rowblocks(int64_t m, int64_t n, int64_t k, bool pre, Plan8& p)
   // x 2048 15.9 -> 17.5, 2048 x 1536 x 4096 26.4 -> 32.1), and K = 8192 gained 4% (512 x 1536 x 8192).
   // Their K splits keep >= 16 K blocks each: 300 x 512 x 2048 on 2 splits 7.01, on one 6.53 (80
   // workgroups); 512 x 512 x 4096 on 2 splits 8.73, on one 9.96 (128); 1024 x 256 x 4096 9.11 and 9.92.
+  // (The K-group blocks below come first where they fit, from 8 K blocks: several of these shapes now
+  // take them.)
   if (m > 256 && (!pre || KB < 8 || KB > 32)) return false;
   // m = 33..128 on 16..32 K blocks (preshuffled weights): 32-row blocks whose 4 waves split K among
   // themselves (4 groups of one wave, 16 columns, while that makes <= 256 workgroups; else 2 groups of
